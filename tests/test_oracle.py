@@ -298,6 +298,60 @@ def test_qkv_post_rotation_invariants():
         assert not np.array_equal(fa, fb)
 
 
+def _rope_closed_form(normalized, position, dimension, theta, rotating_pairs):
+    """Rotate-half RoPE of qkv.cu:410-416 in float64: for i < D/2 with frequency
+    f_i = theta^(-2i/D), out[i] = n[i]cos(p f_i) - n[i+D/2]sin(p f_i) and
+    out[i+D/2] = n[i+D/2]cos(p f_i) + n[i]sin(p f_i); pairs i >= rotating_pairs stay as they are."""
+    half = dimension // 2
+    out = normalized.copy()
+    for i in range(min(half, rotating_pairs)):
+        angle = position * theta ** (-2.0 * i / dimension)
+        c, s = math.cos(angle), math.sin(angle)
+        a, b = normalized[..., i], normalized[..., i + half]
+        out[..., i] = a * c - b * s
+        out[..., i + half] = b * c + a * s
+    return out
+
+
+@pytest.mark.parametrize("proportional", [False, True], ids=["sliding", "global_partial"])
+@pytest.mark.parametrize("key_equals_value", [False, True], ids=["kv", "k_eq_v"])
+def test_qkv_post_closed_form_rotation(proportional, key_equals_value):
+    """Known answers for qkv.cu:387-530 at nonzero positions: weighted per-head RMSNorm, then the
+    rotate-half rotation in its stated sense (a flipped sign moves values by ~|n sin|), partial
+    rotary of D/8 pairs in global layers (qkv.cu:52-55), V = unweighted RMSNorm of the V input,
+    which is the K input in K=V mode."""
+    rng = np.random.default_rng(21)
+    hq, hkv, d = 4, 2, 128
+    rows = 4
+    width = (hq + hkv * (1 if key_equals_value else 2)) * d
+    packed = oracle.f32_to_bf16(rng.standard_normal((rows, width)) * 3.0)
+    qw = oracle.f32_to_bf16(1.0 + 0.5 * rng.standard_normal(d))
+    kw = oracle.f32_to_bf16(1.0 + 0.5 * rng.standard_normal(d))
+    positions = np.array([17, 1, 300, 4095], np.int32)
+    cos, sin = oracle.rope_table(d, proportional, 4096)
+    q, k, v = oracle.qkv_post(packed, qw, kw, cos, sin, positions, hq, hkv, d, key_equals_value)
+    f = lambda a: oracle.bf16_to_f32(a).astype(np.float64)
+    heads = f(packed).reshape(rows, -1, d)
+    rms = lambda x: x / np.sqrt((x ** 2).mean(-1, keepdims=True) + 1e-6)
+    theta, pairs = (1e6, d // 8) if proportional else (1e4, d // 2)
+    k_in = heads[:, hq:hq + hkv]
+    v_in = k_in if key_equals_value else heads[:, hq + hkv:]
+    for r in range(rows):
+        eq = _rope_closed_form(rms(heads[r, :hq]) * f(qw), int(positions[r]), d, theta, pairs)
+        ek = _rope_closed_form(rms(k_in[r]) * f(kw), int(positions[r]), d, theta, pairs)
+        for got, exp in ((f(q[r]), eq), (f(k[r]), ek)):
+            # bf16 rounding of the normalized value, of cos/sin and of the output: a few bf16 ulps
+            assert np.abs(got - exp).max() <= 4 * 2 ** -8 * np.abs(exp).max(), r
+        assert np.allclose(f(v[r]), rms(v_in[r]), rtol=2 ** -7, atol=1e-6)
+    # the same values with the opposite rotation sense are far off at position 17
+    wrong = _rope_closed_form(rms(heads[0, :hq]) * f(qw), -17, d, theta, pairs)
+    assert np.abs(f(q[0]) - wrong).max() > 0.3
+    if proportional:  # pairs past D/8 do not rotate: the output is the rounded normalized value
+        idx = np.r_[pairs:d // 2, d // 2 + pairs:d]
+        n = oracle.f32_to_bf16(rms(heads[2, :hq]) * f(qw))
+        assert np.array_equal(q[2][..., idx], n[..., idx])
+
+
 # ------------------------------------------------------------------ attention
 def _rand_bf16(rng, shape, scale=1.0):
     return oracle.f32_to_bf16(rng.standard_normal(shape) * scale)
@@ -413,3 +467,55 @@ def test_commit_kv_net_effect_of_backup_and_restore():
     got_k, got_v = cache_k.copy(), cache_v.copy()
     oracle.commit_kv(got_k, got_v, kn, vn, slots, positions, accepted, C)
     assert np.array_equal(got_k, ref_k) and np.array_equal(got_v, ref_v)
+
+
+def _e4m3_pow2_kv(rng, shape):
+    """e4m3 codes of N(0,1)-ish values, finite codes only."""
+    codes = oracle.f32_to_e4m3(rng.standard_normal(shape).astype(np.float32) * 2.0)
+    return codes
+
+
+def test_fp8_attention_equals_bf16_attention_on_exact_dequantised_values():
+    """With power-of-two scales e4m3(x)*scale is exact in bf16 and scaling by 2^k commutes with
+    every fp32 sum, so the e4m3 oracle must equal the bf16 oracle on the dequantised K/V bit for
+    bit (global window, ragged positions including position 0)."""
+    rng = np.random.default_rng(31)
+    R, T, hq, hkv, d, C = 3, 5, 4, 2, 32, 48
+    positions = np.array([0, 7, 40], np.int32)
+    slots = np.array([2, 0, 1], np.int32)
+    table = oracle.e4m3_table().astype(np.float32)
+    kc, vc = _e4m3_pow2_kv(rng, (3, hkv, C, d)), _e4m3_pow2_kv(rng, (3, hkv, C, d))
+    kn, vn = _e4m3_pow2_kv(rng, (R, T, hkv, d)), _e4m3_pow2_kv(rng, (R, T, hkv, d))
+    q = _rand_bf16(rng, (R, T, hq, d), 0.25)
+    for k_scale, v_scale in ((0.25, 2.0), (1.0, 0.0625)):
+        deq = lambda codes, s: oracle.f32_to_bf16(table[codes] * np.float32(s))
+        for codes, s in ((kc, k_scale), (vc, v_scale), (kn, k_scale), (vn, v_scale)):
+            assert np.array_equal(oracle.bf16_to_f32(deq(codes, s)), table[codes] * np.float32(s))
+        got = oracle.verify_attention_fp8(q, kc, vc, kn, vn, k_scale, v_scale, slots, positions, C)
+        exp = oracle.verify_attention(q, deq(kc, k_scale), deq(vc, v_scale), deq(kn, k_scale),
+                                      deq(vn, v_scale), slots, positions, C, 0)
+        assert np.array_equal(got, exp)
+
+
+def test_fp8_attention_brute_force():
+    """Any scales: float64 softmax over e4m3(k)*s_k with output sum p*e4m3(v)*s_v."""
+    rng = np.random.default_rng(32)
+    R, T, hq, hkv, d, C = 2, 3, 4, 1, 16, 24
+    positions = np.array([3, 20], np.int32)
+    slots = np.array([1, 0], np.int32)
+    table = oracle.e4m3_table().astype(np.float64)
+    kc, vc = _e4m3_pow2_kv(rng, (2, hkv, C, d)), _e4m3_pow2_kv(rng, (2, hkv, C, d))
+    kn, vn = _e4m3_pow2_kv(rng, (R, T, hkv, d)), _e4m3_pow2_kv(rng, (R, T, hkv, d))
+    q = _rand_bf16(rng, (R, T, hq, d), 0.3)
+    ks, vs = 0.0371, 0.113
+    got = oracle.bf16_to_f32(oracle.verify_attention_fp8(q, kc, vc, kn, vn, ks, vs, slots,
+                                                         positions, C)).astype(np.float64)
+    qf = oracle.bf16_to_f32(q).astype(np.float64)
+    for r in range(R):
+        p = int(positions[r])
+        for t in range(T):
+            keys = [table[kc[slots[r], 0, j]] if j < p else table[kn[r, j - p, 0]] for j in range(p + t + 1)]
+            vals = [table[vc[slots[r], 0, j]] if j < p else table[vn[r, j - p, 0]] for j in range(p + t + 1)]
+            for h in range(hq):
+                exp = _softmax_attention(qf[r, t, h], np.array(keys) * ks, np.array(vals) * vs)
+                assert np.allclose(got[r, t, h], exp, rtol=2 ** -7, atol=2 ** -8 * np.abs(exp).max())
