@@ -623,6 +623,19 @@ static int linear_common(bool fp8, const uint16_t *x, int m, int k, const float 
   });
 }
 
+int carat_hip_gemm_plan(int n, int k, int fp8, int gate_up, int *tiles_per_wave, int *waves,
+                        int *splits) {
+  return guarded([&] {
+    if (n <= 0 || k <= 0) throw std::runtime_error("invalid skinny GEMM shape");
+    const WeightLayout l = gemm_weight_layout(n, k * (fp8 ? 1 : 2), gate_up != 0);
+    if (tiles_per_wave != nullptr) *tiles_per_wave = l.tiles_per_wave;
+    if (waves != nullptr) *waves = l.waves;
+    // gate/up feeds the GELU epilogue, which needs whole sums: it never splits K
+    if (splits != nullptr)
+      *splits = gate_up ? 1 : gemm_choose_splits(gemm_blocks_n(l), l.row_bytes / 128);
+  });
+}
+
 int carat_hip_fp8_linear(const uint16_t *x, int m, int k, const float *x_amax, const uint8_t *w,
                          int n, const float *w_scale, int epilogue, int splits, uint16_t *y,
                          float *y_amax, float *partial, int32_t *predictions, void *stream) {

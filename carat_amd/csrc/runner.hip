@@ -1638,6 +1638,8 @@ struct BatchModelRunner::Implementation {
     if (name == "assistant.pre_projection") return give_packed(a_pre_projection);
     if (name == "assistant.post_projection") return give_packed(a_post_projection);
     if (name == "assistant.final_norm") return give(a_final_norm);
+    // the last draft step's post-projection output ([batch][hidden] bf16, rows < active valid)
+    if (name == "assistant.previous_hidden") return give(a_previous_hidden);
     const auto dot = name.find('.');
     const auto dot2 = name.find('.', dot + 1);
     if (dot != std::string::npos && dot2 != std::string::npos) {

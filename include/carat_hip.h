@@ -216,6 +216,11 @@ int carat_hip_argmax_accept(const float *logits_f32, const uint16_t *logits_bf16
 int carat_hip_fp8_linear(const uint16_t *x, int m, int k, const float *x_amax, const uint8_t *w,
                          int n, const float *w_scale, int epilogue, int splits, uint16_t *y,
                          float *y_amax, float *partial, int32_t *predictions, void *stream);
+/* No reference counterpart (cuBLASLt picks its own algorithm, linear.cu:53-72): the storage layout
+ * (tiles per wave, waves per workgroup) and split-K factor the runner uses for an [n][k] weight,
+ * so op-level calls can reproduce the runner's exact dispatch. */
+int carat_hip_gemm_plan(int n, int k, int fp8, int gate_up, int *tiles_per_wave, int *waves,
+                        int *splits);
 /* Bf16Linear::run (linear.cu:534-643), same epilogues (no scales). */
 int carat_hip_bf16_linear(const uint16_t *x, int m, int k, const uint16_t *w, int n, int epilogue,
                           int splits, uint16_t *y, float *y_amax, float *partial,

@@ -235,24 +235,68 @@ float orc_quantize_e4m3(const uint16_t *x, int64_t n, float scale_multiplier, ui
   return scale;
 }
 
+/* Shared by the fp8 and bf16 GEMMs: out[row][col] = s * sum_k x[row][k] * w[col][k] over
+ * float operands, accumulated in double per output (so the summation order does not matter at
+ * the tolerance the tests use). Four token rows share each weight row pass. */
+static void linear_f32_rows(const float *xf, int m, int k,
+                            int n, float s, float *out, const uint8_t *qw, const float *table,
+                            const uint16_t *bw) {
+#pragma omp parallel
+  {
+    float *wrow = (float *)malloc(sizeof(float) * (size_t)(k > 0 ? k : 1));
+#pragma omp for schedule(static)
+    for (int col = 0; col < n; ++col) {
+      if (qw)
+        for (int kk = 0; kk < k; ++kk) wrow[kk] = table[qw[(int64_t)col * k + kk]];
+      else
+        for (int kk = 0; kk < k; ++kk) wrow[kk] = orc_bf16_to_f32(bw[(int64_t)col * k + kk]);
+      int row = 0;
+      for (; row + 4 <= m; row += 4) {
+        const float *x0 = xf + (int64_t)row * k, *x1 = x0 + k, *x2 = x1 + k, *x3 = x2 + k;
+        double a0 = 0.0, a1 = 0.0, a2 = 0.0, a3 = 0.0;
+        for (int kk = 0; kk < k; ++kk) {
+          const double w = wrow[kk];
+          a0 += (double)x0[kk] * w;
+          a1 += (double)x1[kk] * w;
+          a2 += (double)x2[kk] * w;
+          a3 += (double)x3[kk] * w;
+        }
+        out[(int64_t)row * n + col] = (float)a0 * s;
+        out[(int64_t)(row + 1) * n + col] = (float)a1 * s;
+        out[(int64_t)(row + 2) * n + col] = (float)a2 * s;
+        out[(int64_t)(row + 3) * n + col] = (float)a3 * s;
+      }
+      for (; row < m; ++row) {
+        const float *xr = xf + (int64_t)row * k;
+        double acc = 0.0;
+        for (int kk = 0; kk < k; ++kk) acc += (double)xr[kk] * wrow[kk];
+        out[(int64_t)row * n + col] = (float)acc * s;
+      }
+    }
+    free(wrow);
+  }
+}
+
 void orc_fp8_linear_f32(const uint8_t *qx, float sx, const uint8_t *qw, float sw, int m, int k,
                         int n, float *out) {
   float table[256];
   for (int i = 0; i < 256; ++i) table[i] = orc_e4m3_to_f32((uint8_t)i);
   float *xf = (float *)malloc(sizeof(float) * (size_t)m * k);
   for (int64_t i = 0; i < (int64_t)m * k; ++i) xf[i] = table[qx[i]];
-  const float s = sx * sw;
-#pragma omp parallel for schedule(static)
-  for (int col = 0; col < n; ++col) {
-    float wrow[k > 0 ? k : 1];
-    for (int kk = 0; kk < k; ++kk) wrow[kk] = table[qw[(int64_t)col * k + kk]];
-    for (int row = 0; row < m; ++row) {
-      const float *xr = xf + (int64_t)row * k;
-      double acc = 0.0;
-      for (int kk = 0; kk < k; ++kk) acc += (double)xr[kk] * wrow[kk];
-      out[(int64_t)row * n + col] = (float)acc * s;
-    }
-  }
+  linear_f32_rows(xf, m, k, n, sx * sw, out, qw, table, NULL);
+  free(xf);
+}
+
+/* Bf16Linear::run (linear.cu:534-643; cuBLASLt bf16 GEMM, fp32 accumulation, bf16 output):
+ * Y[m][n] = bf16(sum_k x[m][k] * w[n][k]). The assistant's projections and lm_head
+ * (assistant_runner.cu:147-160, AssistantFp8Mode::off). */
+void orc_bf16_linear(const uint16_t *x, const uint16_t *w, int m, int k, int n, uint16_t *out) {
+  float *xf = (float *)malloc(sizeof(float) * (size_t)m * k);
+  float *tmp = (float *)malloc(sizeof(float) * (size_t)m * n);
+  for (int64_t i = 0; i < (int64_t)m * k; ++i) xf[i] = orc_bf16_to_f32(x[i]);
+  linear_f32_rows(xf, m, k, n, 1.0f, tmp, NULL, NULL, w);
+  for (int64_t i = 0; i < (int64_t)m * n; ++i) out[i] = orc_f32_to_bf16(tmp[i]);
+  free(tmp);
   free(xf);
 }
 

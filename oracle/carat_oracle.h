@@ -21,8 +21,13 @@
  *   orc_fp8_linear         -- float64 numpy matmul over the same e4m3 bytes. Parity with the
  *        reference's cuBLASLt kernel is tolerance-only (closed library).
  *   norms / gelu / embedding / qkv / rope -- numpy float64 closed forms.
+ *   orc_bf16_linear        -- float64 numpy matmul over the same bf16 operands.
+ *   orc_qkv_post           -- float64 closed form of the rotate-half rotation in its stated sense
+ *        at nonzero positions, partial rotary (global D/8 pairs) and K=V mode.
  *   orc_verify_attention   -- the reference's own ring+backup formulation restated separately
  *        (orc_ring_backup_attention, cuda_ops_tests.cu:1630-1779) and numpy brute force.
+ *   orc_verify_attention_fp8 -- bit-equal to orc_verify_attention on dequantised K/V under
+ *        power-of-two scales (exact in bf16), and numpy brute force under any scales.
  *   orc_decode_attention   -- numpy brute force softmax attention.
  */
 #ifndef CARAT_ORACLE_H
@@ -70,6 +75,8 @@ void orc_fp8_linear(const uint8_t *qx, float sx, const uint8_t *qw, float sw, in
                     uint16_t *out);
 void orc_fp8_linear_f32(const uint8_t *qx, float sx, const uint8_t *qw, float sw, int m, int k,
                         int n, float *out);
+/* Bf16Linear::run (linear.cu:534-643): bf16 output of an fp32-accumulated GEMM. */
+void orc_bf16_linear(const uint16_t *x, const uint16_t *w, int m, int k, int n, uint16_t *out);
 /* lm_head restatement: quantize x, fp8 GEMM, bf16 logits, argmax. */
 void orc_fp8_lm_head_argmax(const uint16_t *x, int m, int k, const uint8_t *qw, float sw, int n,
                             int32_t *argmax_out, uint16_t *logits_out /* nullable */);

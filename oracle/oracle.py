@@ -192,6 +192,16 @@ def fp8_linear_f32(qx, sx, qw, sw) -> np.ndarray:
     return out
 
 
+def bf16_linear(x_bf16, w_bf16) -> np.ndarray:
+    x = c(x_bf16, np.uint16)
+    w = c(w_bf16, np.uint16)
+    m, k = x.shape
+    n = w.shape[0]
+    out = np.empty((m, n), np.uint16)
+    lib().orc_bf16_linear(p(x), p(w), m, k, n, p(out))
+    return out
+
+
 def fp8_lm_head_argmax(x_bf16, qw, sw):
     x = c(x_bf16, np.uint16)
     qw = c(qw, np.uint8)

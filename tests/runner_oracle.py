@@ -1,7 +1,9 @@
-"""Oracle composition of one verify step of the runner (test helper).
+"""Oracle compositions of the runner's verify step and assistant draft (test helpers).
 
-Restates cuda/batch_model_runner.cu:1617-1810 with cuda/layer_runner.cu:241-354,730-1041 using the
-oracle primitives, on the weights and caches read back from a BatchModelRunner.
+verify_step restates cuda/batch_model_runner.cu:1617-1810 with cuda/layer_runner.cu:241-354,
+730-1041; draft_steps restates cuda/assistant_runner.cu:162-338 (with batch_model_runner.cu:
+1813-1836 for its arguments). Both use the oracle primitives on the weights and caches read back
+from a BatchModelRunner.
 """
 import math
 
@@ -70,4 +72,92 @@ def verify_step(runner, desc, batch, capacity_of, proposals, slots, positions):
     pred, logits = oracle.fp8_lm_head_argmax(x, emb_q, emb_s)
     out["predictions"] = pred
     out["logits"] = logits
+    return out
+
+
+def _shared_layers(desc):
+    """batch_model_runner.cu shared_sliding_layer / shared_global_layer: the target's last sliding
+    and last global layers, whose caches the assistant reads."""
+    last_sliding = max(i for i, l in enumerate(desc.layers) if l.sliding)
+    last_global = max(i for i, l in enumerate(desc.layers) if not l.sliding)
+    return last_sliding, last_global
+
+
+def draft_steps(runner, desc, batch, capacity_of, last_tokens, slots, forced=None, depth=4,
+                feed=None):
+    """One draft_four call (assistant_runner.cu:218-338), bf16 projections (AssistantFp8Mode::off).
+
+    Per step: input = [embedding(token) * bf16(sqrt(H)) | previous hidden], pre-projection, the
+    assistant layers (run_layer, :162-208: q-only projection, query RMSNorm + RoPE at position
+    context + step, decode attention over the target's last sliding / global cache with
+    valid = min(context + 1, C), o, norms, gate/up GELU, down), final norm, lm_head + argmax
+    (the forced token instead at step 0 when given, :306-312), post-projection -> previous hidden.
+    context = slot position - 1 (batch_model_runner.cu:1820-1828). With `feed` ([rows][depth]),
+    step d > 0 takes feed[:, d - 1] as its input token instead of the oracle's own output
+    (teacher forcing), so a GPU chain can be checked step by step.
+
+    Returns dict(tokens [rows][depth], logits [depth] (None at a forced step), hidden [depth]).
+    """
+    H = desc.hidden
+    AH = desc.assistant_hidden
+    rows = len(last_tokens)
+    slots = np.asarray(slots, np.int32)
+    context = np.array([runner.slot_position(int(s)) - 1 for s in slots], np.int32)
+    emb = runner.read("token_embedding", np.uint16).reshape(desc.vocabulary, H)
+    a_emb = runner.read("assistant.token_embedding", np.uint16).reshape(desc.vocabulary, AH)
+    pre_w = runner.read("assistant.pre_projection", np.uint16).reshape(AH, 2 * H)
+    post_w = runner.read("assistant.post_projection", np.uint16).reshape(H, AH)
+    final_norm = runner.read("assistant.final_norm", np.uint16)
+    previous = runner.read("target_hidden", np.uint16).reshape(batch, H)[slots]
+    last_sliding, last_global = _shared_layers(desc)
+    layers = []
+    for li in range(desc.assistant_layers):
+        pre = f"assistant.layer.{li}."
+        glob = li == desc.assistant_layers - 1
+        target = last_global if glob else last_sliding
+        spec = desc.layers[target]
+        D, hkv, hq = spec.head_dimension, spec.kv_heads, desc.assistant_query_heads
+        C = capacity_of(target)
+        w = {n: runner.read(pre + n, np.uint16) for n in
+             ("input_norm", "q_norm", "post_attention_norm", "pre_mlp_norm", "post_mlp_norm", "scalar")}
+        w["q"] = runner.read(pre + "q", np.uint16).reshape(hq * D, AH)
+        w["o"] = runner.read(pre + "o", np.uint16).reshape(AH, hq * D)
+        w["gate_up"] = runner.read(pre + "gate_up", np.uint16).reshape(2 * desc.assistant_intermediate, AH)
+        w["down"] = runner.read(pre + "down", np.uint16).reshape(AH, desc.assistant_intermediate)
+        kind = "global" if glob else "sliding"
+        w["cos"] = runner.read(f"rope.{kind}.cos", np.uint16).reshape(-1, D)
+        w["sin"] = runner.read(f"rope.{kind}.sin", np.uint16).reshape(-1, D)
+        w["k"] = runner.read(f"cache.{target}.k", np.uint16).reshape(batch, hkv, C, D)
+        w["v"] = runner.read(f"cache.{target}.v", np.uint16).reshape(batch, hkv, C, D)
+        layers.append((w, D, hkv, hq, C))
+    tokens = np.asarray(last_tokens, np.int32)
+    out = {"tokens": np.zeros((rows, depth), np.int32), "logits": [], "hidden": []}
+    for d in range(depth):
+        x = oracle.embedding(emb, tokens, math.sqrt(H))
+        h = oracle.bf16_linear(np.concatenate([x, previous], axis=1), pre_w)
+        for w, D, hkv, hq, C in layers:
+            n, _ = oracle.rms_norm(h, w["input_norm"], eps=desc.rms_norm_epsilon)
+            qp = oracle.bf16_linear(n, w["q"])
+            q, _, _ = oracle.qkv_post(qp, w["q_norm"], w["q_norm"], w["cos"], w["sin"], context + d,
+                                      hq, 0, D, False, desc.rms_norm_epsilon)
+            attn = oracle.decode_attention(q, w["k"], w["v"], slots, context, hkv, C)
+            o = oracle.bf16_linear(attn.reshape(rows, hq * D), w["o"])
+            r1, pre_mlp, _ = oracle.rms_norm_add_and_norm(o, w["post_attention_norm"], h,
+                                                          w["pre_mlp_norm"], desc.rms_norm_epsilon)
+            act, _ = oracle.gelu_tanh_gate_rows(oracle.bf16_linear(pre_mlp, w["gate_up"]))
+            down = oracle.bf16_linear(act, w["down"])
+            h = oracle.rms_norm_add_scale(down, w["post_mlp_norm"], r1, int(w["scalar"][0]),
+                                          desc.rms_norm_epsilon)
+        fh, _ = oracle.rms_norm(h, final_norm, eps=desc.rms_norm_epsilon)
+        if d == 0 and forced is not None:
+            step_tokens = np.asarray(forced, np.int32)
+            out["logits"].append(None)
+        else:
+            logits = oracle.bf16_linear(fh, a_emb)
+            step_tokens = oracle.argmax_bf16_rows(logits)
+            out["logits"].append(logits)
+        out["tokens"][:, d] = step_tokens
+        previous = oracle.bf16_linear(fh, post_w)
+        out["hidden"].append(previous)
+        tokens = step_tokens if feed is None else np.asarray(feed, np.int32)[:, d]
     return out

@@ -58,3 +58,22 @@ def test_errors_come_back_as_messages():
     assert b"invalid acceptance cap arguments" in lib.carat_hip_last_error()
     with pytest.raises(_lib.CaratError):
         _lib.check(lib.carat_hip_runner_batch(None, ctypes.byref(out)))
+
+
+def test_gemm_plan_is_the_runner_dispatch():
+    """The layouts and split-K factors the runner uses at the verify shapes (host-only query)."""
+    lib = _lib.lib()
+
+    def plan(n, k, fp8, gate_up):
+        f, w, s = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+        _lib.check(lib.carat_hip_gemm_plan(n, k, fp8, gate_up, ctypes.byref(f), ctypes.byref(w),
+                                           ctypes.byref(s)))
+        return f.value, w.value, s.value
+
+    assert plan(8192, 5376, 1, 0) == (1, 4, 2)       # qkv
+    assert plan(5376, 4096, 1, 0) == (1, 4, 2)       # o
+    assert plan(43008, 5376, 1, 1) == (4, 3, 1)      # gate/up (GELU epilogue: no split-K)
+    assert plan(5376, 21504, 1, 0) == (1, 4, 3)      # down
+    assert plan(262144, 5376, 1, 0) == (4, 4, 1)     # lm_head
+    with pytest.raises(_lib.CaratError):
+        _lib.check(lib.carat_hip_gemm_plan(100, 5376, 1, 0, None, None, None))

@@ -1,0 +1,258 @@
+"""Parity at the graded shapes (BASELINE configs 4 and 5) on the GPU.
+
+- Config 4: the fp8 GEMMs at exactly the runner's dispatch (weight layout and split-K factor from
+  carat_hip_gemm_plan): qkv 5376->8192, o 4096->5376, gate/up 5376->2x21504 with the GELU
+  epilogue, down 21504->5376, and the tied lm_head 5376->262144 with its fused argmax, all at
+  M = 120 against the oracle's fp32-accumulated GEMM over the same e4m3 bytes
+  (linear.cu:780-803, batch_model_runner.cu:840-853).
+- Config 5: a verify step of a two-layer (one sliding, one global) model at full Gemma-4-31B
+  benchmark dimensions (hidden 5376, intermediate 21504, vocabulary 262144, 32/16 heads x 128,
+  window 1024) with 24 slots at contexts U[1024, 8187] against tests/runner_oracle.verify_step,
+  and one draft step of the full-size assistant against tests/runner_oracle.draft_steps.
+
+Bars: acceptance, bonus tokens, cache commit and hidden hand-off bit-exact given the GPU's own
+predictions; K/V rows and activations within 3e-2 of the row maximum; every argmax mismatch
+against the oracle a near-tie (gap <= 2 bf16 ulps of the row maximum), mismatch rate printed and
+bounded.
+"""
+import math
+import sys
+
+import numpy as np
+import pytest
+from scipy.special import ndtri
+
+from carat_amd import _lib
+from carat_amd.runner import BatchModelRunner, LayerSpec, ModelDesc
+from oracle import oracle
+from tests.runner_oracle import draft_steps, verify_step
+
+pytestmark = pytest.mark.gpu
+
+H, INTER, VOCAB = 5376, 21504, 262144
+M = 120
+T = 5
+SLOTS = 24
+MAX_CONTEXT = 8192
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def e4m3_normal_codes(rng, shape, std=0.02):
+    """e4m3 codes of N(0, std) values under the per-tensor scale std*6/448 (amax ~ 6 std), drawn
+    through a 65536-entry inverse-CDF table so a 1.4 GB lm_head is quick to make."""
+    table = oracle.f32_to_e4m3((ndtri((np.arange(65536) + 0.5) / 65536) * (448 / 6)).astype(np.float32))
+    out = np.empty(shape, np.uint8)
+    flat = out.reshape(-1)
+    step = 1 << 26
+    for start in range(0, flat.size, step):
+        n = min(step, flat.size - start)
+        flat[start:start + n] = table[rng.integers(0, 65536, n, dtype=np.uint16)]
+    return out, std * 6 / 448
+
+
+def plan(n, k, gate_up):
+    f, w, s = (_lib.ctypes.c_int() for _ in range(3))
+    _lib.check(_lib.lib().carat_hip_gemm_plan(n, k, 1, int(gate_up), _lib.ctypes.byref(f),
+                                              _lib.ctypes.byref(w), _lib.ctypes.byref(s)))
+    return f.value, w.value, s.value
+
+
+# name, n, k, gate_up, the runner's (tiles per wave, waves, splits) for that weight
+CONFIG4 = [("qkv", (32 + 2 * 16) * 128, H, False, (1, 4, 2)),
+           ("o", H, 32 * 128, False, (1, 4, 2)),
+           ("gate_up", 2 * INTER, H, True, (4, 3, 1)),
+           ("down", H, INTER, False, (1, 4, 3)),
+           ("lm_head", VOCAB, H, False, (4, 4, 1))]
+
+
+@pytest.mark.parametrize("name,n,k,gate_up,expect_plan", CONFIG4, ids=[c[0] for c in CONFIG4])
+def test_config4_fp8_gemm_at_runner_dispatch(torch_cuda, name, n, k, gate_up, expect_plan):
+    torch = torch_cuda
+    rng = np.random.default_rng(400 + n % 97)
+    assert plan(n, k, gate_up) == expect_plan
+    splits = expect_plan[2]
+    say(f"case: config-4 {name} m={M} k={k} n={n} plan={expect_plan}")
+    x = oracle.f32_to_bf16(rng.standard_normal((M, k)))
+    amax = float(np.abs(oracle.bf16_to_f32(x)).max())
+    qw, sw = e4m3_normal_codes(rng, (n, k))
+    qx, sx = oracle.quantize_e4m3(x)
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    d_x, d_w = dev(x.view(np.int16)), dev(qw)
+    d_amax, d_sw = dev(np.array([amax], np.float32)), dev(np.array([sw], np.float32))
+    stream = _lib.ptr(torch.cuda.current_stream().cuda_stream)
+    lib = _lib.lib()
+
+    def run(epilogue, s=1):
+        width = n // 2 if epilogue == 3 else n
+        y = torch.zeros((M, width), dtype=torch.int16, device="cuda")
+        y_amax = torch.zeros(1, dtype=torch.float32, device="cuda")
+        part = torch.zeros((s, M, n) if epilogue == 1 else (1,), dtype=torch.float32, device="cuda")
+        pred = torch.zeros(M, dtype=torch.int32, device="cuda")
+        _lib.check(lib.carat_hip_fp8_linear(_lib.ptr(d_x), M, k, _lib.ptr(d_amax), _lib.ptr(d_w), n,
+                                            _lib.ptr(d_sw), epilogue, s, _lib.ptr(y), _lib.ptr(y_amax),
+                                            _lib.ptr(part), _lib.ptr(pred), stream))
+        torch.cuda.synchronize()
+        return (y.cpu().numpy().view(np.uint16), float(y_amax.cpu()[0]), part.cpu().numpy(),
+                pred.cpu().numpy())
+
+    ref32 = oracle.fp8_linear_f32(qx, sx, qw, sw).astype(np.float64)
+    tol = lambda r: np.abs(r) * 2 ** -7 + 1e-3 * np.abs(r).max()
+    if gate_up:
+        y, y_amax, _, _ = run(3)
+        ref, _ = oracle.gelu_tanh_gate_rows(oracle.f32_to_bf16(ref32))
+        g = oracle.bf16_to_f32(y).astype(np.float64)
+        r = oracle.bf16_to_f32(ref).astype(np.float64)
+        # gate and up each carry one bf16 rounding: 2e-2 of the row maximum
+        err = np.abs(g - r).max() / np.abs(r).max()
+        say(f"  gelu gate max rel err {err:.2e}")
+        assert err <= 2e-2
+        assert y_amax == np.abs(g).max()
+        return
+    y, y_amax, _, _ = run(0)
+    g = oracle.bf16_to_f32(y).astype(np.float64)
+    assert np.all(np.abs(g - ref32) <= tol(ref32))
+    assert y_amax == np.abs(g).max()
+    if name == "lm_head":
+        _, _, _, pred = run(2)
+        # bit-exact given identical logits, and a near-tie of the oracle's own argmax
+        assert np.array_equal(pred, oracle.argmax_bf16_rows(y))
+        ref_logits = oracle.bf16_to_f32(oracle.f32_to_bf16(ref32)).astype(np.float64)
+        ref_pred = oracle.argmax_bf16_rows(oracle.f32_to_bf16(ref32))
+        gap = ref_logits.max(1) - ref_logits[np.arange(M), pred]
+        say(f"  lm_head argmax mismatches vs oracle {int(np.sum(pred != ref_pred))}/{M}")
+        assert np.all(gap <= 2 * 2 ** -7 * np.abs(ref_logits).max(1))
+        return
+    # the runner's split-K partials, summed by its consumers in fp32
+    _, _, part, _ = run(1, splits)
+    summed = part.sum(0).astype(np.float64) * np.float32(sx * sw)
+    assert np.allclose(summed, ref32, rtol=1e-3, atol=1e-4 * np.abs(ref32).max())
+
+
+# ------------------------------------------------------------------ config 5 at full dimensions
+def full_desc():
+    return ModelDesc(hidden=H, intermediate=INTER, vocabulary=VOCAB, sliding_window=1024,
+                     layers=[LayerSpec(True), LayerSpec(False)], assistant=True, seed=5,
+                     weight_std=0.02)
+
+
+def capacity_of(desc):
+    return lambda li: min(MAX_CONTEXT, desc.sliding_window) if desc.layers[li].sliding else MAX_CONTEXT
+
+
+@pytest.fixture(scope="module")
+def full_model(torch_cuda):
+    desc = full_desc()
+    say("case: full-dimension two-layer runner create (24 slots, context 8192)")
+    runner = BatchModelRunner(desc, SLOTS, MAX_CONTEXT)
+    rng = np.random.default_rng(55)
+    positions = rng.integers(1024, MAX_CONTEXT - T + 1, SLOTS).astype(np.int32)
+    runner.seed_random_cache(int(positions.max()), seed=7, stddev=1 / math.sqrt(128))
+    for slot, p in enumerate(positions):
+        runner.set_slot_position(slot, int(p))
+    yield desc, runner, positions
+    runner.close()
+
+
+def test_config5_verify_step_full_dimensions(full_model):
+    desc, runner, positions_by_slot = full_model
+    rng = np.random.default_rng(56)
+    slots = rng.permutation(SLOTS).astype(np.int32)
+    positions = positions_by_slot[slots]
+    first = rng.integers(0, VOCAB, SLOTS).astype(np.int32)
+    say("case: config-5 greedy chain (4 dry verifies)")
+    chain = np.zeros((SLOTS, T + 1), np.int32)
+    chain[:, 0] = first
+    for t in range(T):
+        props = np.zeros((SLOTS, T), np.int32)
+        props[:, : t + 1] = chain[:, : t + 1]
+        res = runner.verify_greedy_proposals(props.tolist(), first.tolist(), slots.tolist(), [0] * SLOTS)
+        assert res.accepted_tokens == [0] * SLOTS
+        chain[:, t + 1] = np.array(runner.last_predictions, np.int32).reshape(SLOTS, T)[:, t]
+    # proposals: the greedy chain, rejected at a seeded position in most slots
+    proposals = chain[:, :T].copy()
+    reject = rng.integers(0, T + 2, SLOTS)
+    for r in range(SLOTS):
+        if reject[r] < T:
+            proposals[r, reject[r]] = (proposals[r, reject[r]] + 1) % VOCAB
+    li_s, li_g = 0, 1
+    before = {li: (runner.read(f"cache.{li}.k", np.uint16), runner.read(f"cache.{li}.v", np.uint16))
+              for li in (li_s, li_g)}
+    hidden_before = runner.read("target_hidden", np.uint16).reshape(SLOTS, H).copy()
+    say("case: config-5 oracle verify step (CPU)")
+    expect = verify_step(runner, desc, SLOTS, capacity_of(desc), proposals, slots, positions)
+    say("case: config-5 runner verify")
+    res = runner.verify_greedy_proposals(proposals.tolist(), first.tolist(), slots.tolist())
+    pred = np.array(runner.last_predictions, np.int32).reshape(SLOTS, T)
+    acc, nxt = oracle.greedy_accept(proposals, first, pred)
+    assert res.accepted_tokens == acc.tolist() and res.next_tokens == nxt.tolist()
+    for r in range(SLOTS):  # the planted pattern: accepted = first mismatching index
+        assert res.accepted_tokens[r] == (reject[r] if reject[r] < T else T)
+    # predictions: near-ties only, mismatch rate reported
+    logits = oracle.bf16_to_f32(expect["logits"]).astype(np.float64).reshape(M, -1)
+    flat = pred.reshape(-1)
+    gap = logits.max(1) - logits[np.arange(M), flat]
+    mism = int(np.sum(flat != expect["predictions"]))
+    say(f"  config-5 argmax mismatches vs oracle {mism}/{M}, max gap {gap.max():.3e}")
+    assert np.all(gap <= 2 * 2 ** -7 * np.abs(logits).max(1))
+    assert mism <= M // 10
+    # this step's K/V rows and the final hidden rows
+    for li, spec in enumerate(desc.layers):
+        for kind in ("k", "v"):
+            got = oracle.bf16_to_f32(runner.read(f"new.{li}.{kind}", np.uint16)[: M * 16 * 128])
+            want = oracle.bf16_to_f32(expect[f"{kind}_new"][li]).reshape(-1)
+            err = np.abs(got - want).max() / np.abs(want).max()
+            say(f"  layer {li} {kind} rows max rel err {err:.2e}")
+            assert err <= 3e-2, (li, kind, err)
+    fh = oracle.bf16_to_f32(runner.read("final_hidden", np.uint16)[: M * H]).astype(np.float64)
+    efh = oracle.bf16_to_f32(expect["final_hidden"]).reshape(-1).astype(np.float64)
+    err = np.abs(fh - efh).max() / np.abs(efh).max()
+    say(f"  final hidden max rel err {err:.2e}")
+    assert err <= 3e-2
+    # commit: exact cache bytes, hidden hand-off and positions
+    for li in (li_s, li_g):
+        C = capacity_of(desc)(li)
+        k_exp = before[li][0].reshape(SLOTS, 16, C, 128)
+        v_exp = before[li][1].reshape(SLOTS, 16, C, 128)
+        k_new = runner.read(f"new.{li}.k", np.uint16)[: M * 2048].reshape(SLOTS, T, 16, 128)
+        v_new = runner.read(f"new.{li}.v", np.uint16)[: M * 2048].reshape(SLOTS, T, 16, 128)
+        kept = res.accepted_tokens if desc.layers[li].sliding else [T] * SLOTS
+        oracle.commit_kv(k_exp, v_exp, k_new, v_new, slots, positions, kept, C)
+        assert np.array_equal(runner.read(f"cache.{li}.k", np.uint16), k_exp.reshape(-1)), li
+        assert np.array_equal(runner.read(f"cache.{li}.v", np.uint16), v_exp.reshape(-1)), li
+    final_hidden = runner.read("final_hidden", np.uint16)[: M * H].reshape(M, H)
+    hidden_after = runner.read("target_hidden", np.uint16).reshape(SLOTS, H)
+    for r, slot in enumerate(slots):
+        a = res.accepted_tokens[r]
+        want = final_hidden[r * T + a - 1] if a > 0 else hidden_before[slot]
+        assert np.array_equal(hidden_after[slot], want)
+        assert runner.slot_position(int(slot)) == positions[r] + a
+
+
+def test_config5_draft_step_full_dimensions(full_model):
+    """A forced step and one free step of the full-size assistant (hidden 1024, 4 layers, bf16)
+    over the 24 slots' caches, against the oracle chain teacher-forced on the GPU's tokens."""
+    desc, runner, _ = full_model
+    rng = np.random.default_rng(57)
+    slots = rng.permutation(SLOTS).astype(np.int32).tolist()
+    last = rng.integers(0, VOCAB, SLOTS).astype(np.int32).tolist()
+    forced = rng.integers(0, VOCAB, SLOTS).astype(np.int32).tolist()
+    say("case: config-5 draft (depth 2, forced first token)")
+    got = np.array(runner.draft_four(last, slots, forced, 2), np.int32)
+    assert got[:, 0].tolist() == forced
+    exp = draft_steps(runner, desc, SLOTS, capacity_of(desc), last, slots, forced, 2, feed=got)
+    logits = oracle.bf16_to_f32(exp["logits"][1]).astype(np.float64)
+    gap = logits.max(1) - logits[np.arange(SLOTS), got[:, 1]]
+    mism = int(np.sum(got[:, 1] != exp["tokens"][:, 1]))
+    say(f"  draft argmax mismatches vs oracle {mism}/{SLOTS}, max gap {gap.max():.3e}")
+    assert np.all(gap <= 2 * 2 ** -7 * np.abs(logits).max(1))
+    assert mism <= 2
+    hidden = runner.read("assistant.previous_hidden", np.uint16).reshape(SLOTS, H)
+    g = oracle.bf16_to_f32(hidden).astype(np.float64)
+    e = oracle.bf16_to_f32(exp["hidden"][-1]).astype(np.float64)
+    err = np.abs(g - e).max() / np.abs(e).max()
+    say(f"  draft hidden hand-off max rel err {err:.2e}")
+    assert err <= 2e-2

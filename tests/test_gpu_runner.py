@@ -10,7 +10,7 @@ import pytest
 from carat_amd import CaratError
 from carat_amd.runner import BatchModelRunner, LayerSpec, ModelDesc
 from oracle import oracle
-from tests.runner_oracle import verify_step
+from tests.runner_oracle import draft_steps, verify_step
 
 pytestmark = pytest.mark.gpu
 
@@ -98,8 +98,11 @@ def test_verify_step_matches_oracle_and_commits(model, T):
     # target predictions agree with the oracle's (fp32-order differences only move near-ties)
     logits = oracle.bf16_to_f32(expect["logits"]).astype(np.float64).reshape(4 * T, -1)
     gap = logits.max(1) - logits[np.arange(4 * T), pred.reshape(-1)]
-    assert np.mean(pred.reshape(-1) == expect["predictions"]) >= 0.85
-    assert np.all(gap <= 0.05 * logits.std())
+    mism = int(np.sum(pred.reshape(-1) != expect["predictions"]))
+    say(f"  argmax mismatches vs oracle {mism}/{4 * T}, max gap {gap.max():.3e}")
+    # a mismatch is a near-tie: within 2 bf16 ulps of the row maximum
+    assert np.all(gap <= 2 * 2 ** -7 * np.abs(logits).max(1))
+    assert mism <= max(1, 4 * T // 10)
     # this step's K/V rows agree with the oracle's
     for li in range(len(desc.layers)):
         got_k = runner.read(f"new.{li}.k", np.uint16)[: 4 * T * 2 * 128].reshape(4, T, 2, 128)
@@ -183,18 +186,54 @@ def test_reference_error_messages(model):
         runner.draft_four([1, 2], [0, 1], [5])
 
 
-def test_draft_four_shapes_and_forced_token(model):
+def check_draft_against_oracle(runner, desc, batch, capacity, last, slots, forced, depth, label):
+    """draft_four vs the oracle's assistant chain (assistant_runner.cu:218-338), teacher-forced on
+    the GPU's own tokens: every unforced step's token is the oracle argmax or a near-tie of the
+    oracle's bf16 logits, the forced step returns the forced token, and the last step's
+    post-projection (the hidden hand-off to the next step) agrees with the oracle's."""
+    got = np.array(runner.draft_four(last, slots, forced or [], depth), np.int32)
+    assert got.shape == (len(last), depth)
+    exp = draft_steps(runner, desc, batch, capacity, last, slots, forced or None, depth, feed=got)
+    mismatches, total = 0, 0
+    for d in range(depth):
+        if exp["logits"][d] is None:
+            assert got[:, d].tolist() == list(forced)
+            continue
+        logits = oracle.bf16_to_f32(exp["logits"][d]).astype(np.float64)
+        rows = np.arange(len(last))
+        gap = logits.max(1) - logits[rows, got[:, d]]
+        mismatches += int(np.sum(got[:, d] != exp["tokens"][:, d]))
+        total += len(last)
+        # fp32 summation order only moves near-ties: within 2 bf16 ulps of the row maximum
+        assert np.all(gap <= 2 * 2 ** -7 * np.abs(logits).max(1)), (label, d, gap.max())
+    say(f"  {label}: argmax mismatches {mismatches}/{total} (near-ties)")
+    assert mismatches <= max(1, total // 20), label
+    hidden = runner.read("assistant.previous_hidden", np.uint16).reshape(batch, desc.hidden)[: len(last)]
+    g = oracle.bf16_to_f32(hidden).astype(np.float64)
+    e = oracle.bf16_to_f32(exp["hidden"][-1]).astype(np.float64)
+    err = np.abs(g - e).max() / np.abs(e).max()
+    say(f"  {label}: hidden hand-off max rel err {err:.2e}")
+    assert err <= 2e-2, label
+    return got
+
+
+@pytest.mark.parametrize("depth", [1, 4, 8])
+def test_draft_four_matches_oracle_chain(model, depth):
     desc, runner = model
-    reset_state(runner, [30, 40, 50, 60], seed=13)
-    say("case: draft_four")
+    reset_state(runner, [30, 40, 50, 100], seed=13)  # slot 3 has wrapped its sliding ring
     last = [5, 6, 7, 8]
     slots = [3, 1, 0, 2]
-    free = runner.draft_four(last, slots, [], 4)
-    again = runner.draft_four(last, slots, [], 4)
-    assert free == again  # deterministic
-    assert all(0 <= t < desc.vocabulary for row in free for t in row)
-    forced = runner.draft_four(last, slots, [11, 12, 13, 14], 4)
-    assert [row[0] for row in forced] == [11, 12, 13, 14]
+    say(f"case: draft_four vs oracle chain, depth {depth}")
+    free = check_draft_against_oracle(runner, desc, BATCH, capacity_of(desc), last, slots, None,
+                                      depth, "unforced")
+    again = runner.draft_four(last, slots, [], depth)
+    assert free.tolist() == again  # deterministic
+    forced = check_draft_against_oracle(runner, desc, BATCH, capacity_of(desc), last, slots,
+                                        [11, 12, 13, 14], depth, "forced")
+    assert forced[:, 0].tolist() == [11, 12, 13, 14]
+    # a subset of the slots in another order reads the same caches
+    check_draft_against_oracle(runner, desc, BATCH, capacity_of(desc), [9, 10], [2, 0], None,
+                               depth, "two rows")
 
 
 def test_append_ragged_is_one_forced_decode_step(model):

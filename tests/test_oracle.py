@@ -220,6 +220,17 @@ def _bf(x):
     return oracle.bf16_to_f32(oracle.f32_to_bf16(x)).astype(np.float64)
 
 
+def test_bf16_linear_against_float64_matmul():
+    rng = np.random.default_rng(8)
+    for m, k, n in ((1, 64, 3), (7, 256, 33), (24, 1024, 40)):
+        x = oracle.f32_to_bf16(rng.standard_normal((m, k)))
+        w = oracle.f32_to_bf16(rng.standard_normal((n, k)) * 0.05)
+        exp = oracle.bf16_to_f32(x).astype(np.float64) @ oracle.bf16_to_f32(w).astype(np.float64).T
+        got = oracle.bf16_to_f32(oracle.bf16_linear(x, w)).astype(np.float64)
+        # one bf16 rounding of the float64 value (ties and double-rounding aside)
+        assert np.all(np.abs(got - exp) <= np.abs(exp) * 2 ** -8 * 1.01 + 1e-12)
+
+
 def test_rms_norm_closed_form():
     rng = np.random.default_rng(6)
     x = oracle.f32_to_bf16(rng.standard_normal((5, 384)))
