@@ -574,6 +574,65 @@ int carat_hip_argmax_accept(const float *logits_f32, const uint16_t *logits_bf16
   });
 }
 
+// Allocation-free argmax + acceptance: the partial keys live in a file-scope device array of
+// fixed size instead of a workspace the library allocates. Each device holds its own copy;
+// host code reaches it only through the address hipGetSymbolAddress returns on that device
+// (the array's name is a host-side stand-in, not a device address). Every call on one device
+// shares the array, so calls that overlap on one device race. The partial kernel writes every
+// key the final kernel reads, so nothing needs clearing between calls.
+constexpr size_t kNoAllocArgmaxKeys = 65536;  // 512 KiB: e.g. 256 requests x 8 rows x 32 chunks
+static __device__ __align__(256) uint64_t scratch[kNoAllocArgmaxKeys];
+constexpr int kNoAllocMaxDevices = 64;
+std::mutex scratch_mutex;
+uint64_t *scratch_by_device[kNoAllocMaxDevices] = {};
+
+uint64_t *scratch_for_current_device() {
+  int device = 0;
+  hip_check(hipGetDevice(&device), "get device");
+  if (device < 0 || device >= kNoAllocMaxDevices)
+    throw std::runtime_error("allocation-free argmax: device index out of range");
+  std::lock_guard<std::mutex> lock(scratch_mutex);
+  if (scratch_by_device[device] == nullptr) {
+    void *address = nullptr;
+    hip_check(hipGetSymbolAddress(&address, HIP_SYMBOL(scratch)),
+              "resolve the allocation-free argmax scratch");
+    scratch_by_device[device] = static_cast<uint64_t *>(address);
+  }
+  return scratch_by_device[device];
+}
+
+int carat_hip_argmax_accept_noalloc(const float *logits_f32, const uint16_t *logits_bf16,
+                                    int requests, int tokens, int vocabulary,
+                                    const int32_t *proposals, const int32_t *target_first,
+                                    const int32_t *caps, int32_t *predictions, int32_t *accepted,
+                                    int32_t *next_tokens, void *stream) {
+  return guarded([&] {
+    if (requests <= 0 || tokens <= 0 || vocabulary <= 0)
+      throw std::runtime_error("invalid argmax arguments");
+    const size_t keys = static_cast<size_t>(argmax_accept_chunks(vocabulary, logits_f32 != nullptr)) *
+                        static_cast<size_t>(requests) * static_cast<size_t>(tokens);
+    if (keys > kNoAllocArgmaxKeys)
+      throw std::runtime_error("allocation-free argmax: " + std::to_string(keys) +
+                               " partial keys exceed the fixed scratch of " +
+                               std::to_string(kNoAllocArgmaxKeys));
+    ArgmaxAcceptArgs a;
+    a.logits_f32 = logits_f32;
+    a.logits_bf16 = logits_bf16;
+    a.requests = requests;
+    a.tokens = tokens;
+    a.vocabulary = vocabulary;
+    a.proposals = proposals;
+    a.target_first = target_first;
+    a.caps = caps;
+    a.predictions = predictions;
+    a.accepted = accepted;
+    a.next_tokens = next_tokens;
+    a.partials = scratch_for_current_device();
+    a.partial_capacity = kNoAllocArgmaxKeys;
+    launch_argmax_accept(a, static_cast<hipStream_t>(stream));
+  });
+}
+
 static int linear_common(bool fp8, const uint16_t *x, int m, int k, const float *x_amax,
                          const void *w, int n, const float *w_scale, int epilogue, int splits,
                          uint16_t *y, float *y_amax, float *partial, int32_t *predictions,

@@ -208,6 +208,18 @@ int carat_hip_argmax_accept(const float *logits_f32, const uint16_t *logits_bf16
                             int32_t *predictions, int32_t *accepted, int32_t *next_tokens,
                             void *stream);
 
+/* No counterpart in the reference. For callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc): carat_hip_argmax_accept
+ * with its partial keys in a fixed per-device scratch array (64 Ki keys, 512 KiB) instead of a
+ * library-allocated workspace. Calls no hipMalloc/hipFree. Rejects shapes needing more than 65536
+ * keys (ceil(vocabulary / 8192) chunks for fp32 logits, / 16384 for bf16, times requests x tokens).
+ * Every call on one device shares that scratch: calls that overlap on one device race. */
+int carat_hip_argmax_accept_noalloc(const float *logits_f32, const uint16_t *logits_bf16,
+                                    int requests, int tokens, int vocabulary,
+                                    const int32_t *proposals, const int32_t *target_first,
+                                    const int32_t *caps, int32_t *predictions, int32_t *accepted,
+                                    int32_t *next_tokens, void *stream);
+
 /* Fp8Linear::run (linear.h, linear.cu:780-803) with the activation quantisation of
  * quantize_bf16_to_fp8_e4m3_from_amax_values (linear.cu:273-296) fused: x bf16 [m][k], x_amax
  * device float (producer amax), w e4m3 [n][k], w_scale device float.

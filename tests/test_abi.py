@@ -77,3 +77,13 @@ def test_gemm_plan_is_the_runner_dispatch():
     assert plan(262144, 5376, 1, 0) == (4, 4, 1)     # lm_head
     with pytest.raises(_lib.CaratError):
         _lib.check(lib.carat_hip_gemm_plan(100, 5376, 1, 0, None, None, None))
+
+
+def test_noalloc_argmax_rejects_shapes_beyond_its_scratch():
+    """The size check runs before any device call, so it is testable without a GPU."""
+    lib = _lib.lib()
+    # 512 requests x 8 rows x 32 fp32 chunks = 131072 keys > 65536
+    status = lib.carat_hip_argmax_accept_noalloc(ctypes.c_void_p(16), None, 512, 8, 262144, None,
+                                                 None, None, None, None, None, None)
+    assert status != 0
+    assert b"exceed the fixed scratch of 65536" in lib.carat_hip_last_error()
