@@ -4,7 +4,8 @@
 Workload: a random-init Gemma-4-31B-shaped FP8 target (60 layers, 5 sliding(1024) : 1 global,
 hidden 5376, intermediate 21504, 32 query / 16 KV heads x 128, vocab 262144) and a random-init
 4-layer assistant (hidden 1024 on the 5376 backbone, the reference's assistant dims), 24 slots with
-~8.1k-token contexts. One step = the reference scheduler's speculative cycle
+~8.1k-token contexts, prefilled (untimed) from seeded random token ids through the runner's own
+prefill_slots_chunks. One step = the reference scheduler's speculative cycle
 (native_runtime_main.cpp:583-678): draft_four (forced + 4 drafts) -> acceptance caps ->
 verify_greedy_proposals -> commit_speculation. Drafts are overwritten, before verification, with
 the target's own greedy chain (computed untimed by dry verifies that commit nothing) so that each
@@ -42,6 +43,24 @@ ACCEPT_P = 0.7
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
+
+
+def prefill_contexts(runner, rng, vocab, length):
+    """Config 5's contexts: `length` seeded random token ids per slot, made resident with
+    prefill_slots_chunks (forced verify steps sharing the 1024-row step budget). Returns the
+    target's greedy next token per slot (the first forced token) and each prompt's last token."""
+    slots = list(range(SLOTS))
+    prompts = [rng.integers(0, vocab, length).astype(np.int32).tolist() for _ in slots]
+    for s in slots:
+        runner.reset_slot(s)
+    # each call packs at most the context's worth of chunk tokens (batch_model_runner.cu:1262);
+    # a multiple of the 42 rows per slot that a 1024-row step gives 24 slots
+    per_step = 1024 // SLOTS
+    quantum = MAX_CONTEXT // SLOTS // per_step * per_step
+    out = [None]
+    while any(v is None for v in out):
+        out = runner.prefill_slots_chunks(slots, prompts, quantum)
+    return np.array(out, np.int32), np.array([p[-1] for p in prompts], np.int32)
 
 
 def planted_proposals(runner, forced, slots, rng, vocab):
@@ -362,6 +381,9 @@ def main() -> int:
     ap.add_argument("--native", action="store_true",
                     help="the same step at the native Gemma-4 31B attention geometry (sliding D 256, "
                          "global D 512 with 4 kv heads and K = V) instead of config 5's D 128")
+    ap.add_argument("--seeded-cache", action="store_true",
+                    help="fill the KV caches with seeded N(0, 1/D) values instead of prefilling "
+                         "the contexts from seeded random token ids (same bytes, faster set-up)")
     ap.add_argument("--prefill", type=int, default=0, metavar="TOKENS",
                     help="time prefill_slots_chunks of TOKENS-token prompts on all 24 slots of the "
                          "config-5 model instead of the step")
@@ -399,13 +421,18 @@ def main() -> int:
     rng = np.random.default_rng(args.seed)
     t0 = time.perf_counter()
     runner = BatchModelRunner(desc, SLOTS, MAX_CONTEXT)
-    runner.seed_random_cache(start_position, seed=args.seed,
-                             stddev=1 / math.sqrt(256 if args.native else 128))
     log(f"runner ready in {time.perf_counter() - t0:.1f}s; contexts start at {start_position}")
-    runner.set_graphs(args.graphs)
     slots = list(range(SLOTS))
-    forced = rng.integers(0, desc.vocabulary, SLOTS).astype(np.int32)
-    last = rng.integers(0, desc.vocabulary, SLOTS).astype(np.int32)
+    if args.seeded_cache:
+        runner.seed_random_cache(start_position, seed=args.seed,
+                                 stddev=1 / math.sqrt(256 if args.native else 128))
+        forced = rng.integers(0, desc.vocabulary, SLOTS).astype(np.int32)
+        last = rng.integers(0, desc.vocabulary, SLOTS).astype(np.int32)
+    else:
+        t0 = time.perf_counter()
+        forced, last = prefill_contexts(runner, rng, desc.vocabulary, start_position)
+        log(f"prefilled {SLOTS} x {start_position} tokens in {time.perf_counter() - t0:.1f}s")
+    runner.set_graphs(args.graphs)
     remaining = 1 << 20
 
     timed_s = 0.0
@@ -477,7 +504,9 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp8",
-        "data": "synthetic (seeded random weights, KV caches and tokens; no checkpoint)",
+        "data": ("synthetic (seeded random weights and tokens; KV caches "
+                 + ("seeded N(0,1/D) values" if args.seeded_cache else
+                    "prefilled from seeded random token ids") + "; no checkpoint)"),
         "config": {
             "workload": ("native-geometry" if args.native else "config5") +
                         " end-to-end speculative step: 4-layer assistant draft + 60-layer "
@@ -486,6 +515,8 @@ def main() -> int:
                           else "D128 32/16 heads"),
             "slots": SLOTS, "draft": DRAFTS, "verify_rows": rows, "layers": 60,
             "context_start": start_position, "accept_p": ACCEPT_P,
+            "contexts": ("seeded KV values" if args.seeded_cache
+                         else "prefilled from seeded random token ids"),
             "graphs": bool(args.graphs),
             "mean_accepted_per_step": round(accepted_total / steps, 2),
             "draft_ms": round(draft_ms / steps, 3), "verify_ms": round(verify_ms / steps, 3),

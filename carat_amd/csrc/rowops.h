@@ -102,7 +102,7 @@ struct SlidingLayerKv {
 };
 
 struct AcceptArgs {
-  const int32_t *predictions_in = nullptr;  // [R*T] target argmax of every verified row
+  int32_t *predictions = nullptr;        // [R*T] target argmax of every verified row
   const int32_t *proposals = nullptr;    // [R][T]
   const int32_t *target_first = nullptr; // [R]
   const int32_t *caps = nullptr;         // [R] or nullptr
@@ -121,6 +121,9 @@ struct AcceptArgs {
   int hidden = 0;
   // prefill: every row is accepted (no comparison); next = the prediction after the last row
   bool force_accept = false;
+  // forced steps that ran no lm_head: there are no predictions; the kernel sets every row's
+  // prediction and every next token to -1 instead of reading stale ones
+  bool predictions_missing = false;
 };
 void launch_accept_commit(const AcceptArgs &args, hipStream_t stream);
 

@@ -289,7 +289,14 @@ __global__ __launch_bounds__(256) void accept_commit_kernel(const AcceptArgs a) 
   const int T = a.tokens;
   __shared__ int32_t pred[kMaxAcceptRows];
   __shared__ int accepted_s;
-  for (int t = threadIdx.x; t < T; t += blockDim.x) pred[t] = a.predictions_in[r * T + t];
+  for (int t = threadIdx.x; t < T; t += blockDim.x) {
+    if (a.predictions_missing) {
+      pred[t] = -1;
+      if (part == 0) a.predictions[r * T + t] = -1;
+    } else {
+      pred[t] = a.predictions[r * T + t];
+    }
+  }
   __syncthreads();
   if (threadIdx.x == 0) {
     const int accepted = a.force_accept ? T
@@ -503,7 +510,9 @@ void launch_step_init(float *amax, int amax_count, hipStream_t stream) {
 }
 
 void launch_accept_commit(const AcceptArgs &a, hipStream_t stream) {
-  if (a.predictions_in == nullptr || a.proposals == nullptr || a.target_first == nullptr ||
+  if (a.predictions_missing && !a.force_accept)
+    throw std::runtime_error("only forced steps may run without predictions");
+  if (a.predictions == nullptr || a.proposals == nullptr || a.target_first == nullptr ||
       a.requests <= 0 || a.tokens <= 0 || a.tokens > kMaxAcceptRows ||
       (!a.force_accept && a.tokens > 8) || a.accepted == nullptr ||
       a.next_tokens == nullptr)

@@ -901,9 +901,11 @@ struct BatchModelRunner::Implementation {
   // of each request to the slot when final_hidden is given.
   void enqueue_accept(int requests, int depth, bool has_caps, bool force_accept,
                       const int32_t *positions, const int32_t *slots, int first_sliding,
-                      int sliding_count, const bf16_t *final_rows) {
+                      int sliding_count, const bf16_t *final_rows,
+                      bool predictions_missing = false) {
     AcceptArgs ac;
-    ac.predictions_in = d_predictions;
+    ac.predictions = d_predictions;
+    ac.predictions_missing = predictions_missing;
     ac.proposals = d_tokens;
     ac.target_first = d_first;
     ac.caps = has_caps ? d_caps : nullptr;
@@ -946,13 +948,13 @@ struct BatchModelRunner::Implementation {
       std::swap(io.input, io.output);
     }
     // lm_head + argmax (a forced prefill step whose predictions nobody reads skips it; the
-    // acceptance then reads stale predictions, which the host discards)
+    // acceptance then writes -1 predictions and next tokens)
     if (lm_head_pass)
       run_fp8_gemm(final_hidden.as<bf16_t>(), rows, spec.hidden, lm_head_amax(),
                    lm_head, embedding_scale.as<float>(),
                    GemmEpilogue::argmax, nullptr, nullptr, nullptr, probe_lm_head_gemm);
     enqueue_accept(requests, depth, has_caps, force_accept, d_positions, d_slots, 0,
-                   sliding_layer_count, final_hidden.as<bf16_t>());
+                   sliding_layer_count, final_hidden.as<bf16_t>(), !lm_head_pass);
   }
 
   // batch_model_runner.cu:1544-1615: one decode step per slot at its current position. It is a
@@ -1230,7 +1232,7 @@ struct BatchModelRunner::Implementation {
                      embedding_scale.as<float>(), GemmEpilogue::argmax, nullptr, nullptr, nullptr,
                      probe_lm_head_gemm);
       enqueue_accept(requests, step.depth, false, true, io.positions, io.slots, first_sliding,
-                     sliding_count, complete ? io.normalized : nullptr);
+                     sliding_count, complete ? io.normalized : nullptr, !completes);
       if (completes) {
         std::vector<int32_t> next(static_cast<size_t>(requests));
         hip_check(hipMemcpyAsync(next.data(), d_next, sizeof(int32_t) * next.size(),
@@ -1390,13 +1392,9 @@ struct BatchModelRunner::Implementation {
     int32_t *h_pred = h_next + batch_size;
     GreedyVerificationResult result;
     result.accepted_tokens.assign(h_accepted, h_accepted + requests);
-    if (lm_head_pass) {
-      result.next_tokens.assign(h_next, h_next + requests);
-      predictions.assign(h_pred, h_pred + requests * depth);
-    } else {
-      result.next_tokens.assign(static_cast<size_t>(requests), -1);
-      predictions.assign(static_cast<size_t>(requests) * depth, -1);
-    }
+    // a step without the lm_head reads -1 here: the acceptance kernel wrote it on the device
+    result.next_tokens.assign(h_next, h_next + requests);
+    predictions.assign(h_pred, h_pred + requests * depth);
     for (int r = 0; r < requests; ++r)
       slot_positions[static_cast<size_t>(slots[static_cast<size_t>(r)])] +=
           result.accepted_tokens[static_cast<size_t>(r)];
