@@ -22,7 +22,7 @@ EXPORTED = [
     "carat_hip_runner_prefill_slots_suffix", "carat_hip_runner_prefill_slots_suffix_layer_slice",
     "carat_hip_runner_abort_suffix_layer_slices", "carat_hip_runner_has_suffix_layer_slices",
     "carat_hip_runner_clone_slot", "carat_hip_runner_append",
-    "carat_hip_runner_last_predictions",
+    "carat_hip_runner_last_predictions", "carat_hip_runner_create_from_device_weights",
     "carat_hip_runner_verify", "carat_hip_runner_append_ragged", "carat_hip_runner_draft",
     "carat_hip_runner_has_assistant",
     "carat_hip_runner_batch", "carat_hip_runner_position", "carat_hip_runner_slot_position",

@@ -198,6 +198,20 @@ int carat_hip_runner_create(const carat_hip_model_desc *desc, int batch, int max
   });
 }
 
+int carat_hip_runner_create_from_device_weights(const carat_hip_model_desc *desc,
+                                                carat_hip_device_segment_fn segment,
+                                                void *context, int batch, int maximum_context,
+                                                carat_hip_runner **out) {
+  return guarded([&] {
+    if (out == nullptr) throw std::runtime_error("null output handle");
+    if (segment == nullptr) throw std::runtime_error("missing device weight lookup");
+    auto handle = std::make_unique<carat_hip_runner>();
+    handle->runner = std::make_unique<BatchModelRunner>(spec_from_desc(desc), segment, context,
+                                                        batch, maximum_context);
+    *out = handle.release();
+  });
+}
+
 int carat_hip_checkpoint_describe(const char *model_dir, const char *assistant_dir,
                                   carat_hip_model_desc *desc, carat_hip_layer_desc *layers,
                                   int layer_capacity, uint64_t *target_bytes,

@@ -82,6 +82,17 @@ public:
   // segments are uploaded, fp8 matrices quantised per tensor on the device (amax/448,
   // device_weights.cu:200-263) and packed. The checkpoint is only read during construction.
   BatchModelRunner(const Checkpoint &checkpoint, int batch, int maximum_context);
+  // Weights already on the device (the reference's DeviceWeightArena / Fp8WeightArena,
+  // device_weights.h:15-52): segment(context, assistant, fp8, name, &scale) returns the device
+  // address of the execution segment the reference's WeightPlan names `name`
+  // (weight_plan.cpp:37-189), laid out as that plan lays it out: bf16 when fp8 == 0; e4m3 with
+  // its per-tensor scale (a device float stored to *scale) when fp8 == 1, or null, in which
+  // case the runner quantises the bf16 segment per tensor (amax/448) itself. Segments are copied
+  // device to device and packed; they are only read during construction.
+  using DeviceSegmentFn = const void *(*)(void *context, int assistant, int fp8, const char *name,
+                                          const float **scale);
+  BatchModelRunner(const ModelSpec &spec, DeviceSegmentFn segment, void *context, int batch,
+                   int maximum_context);
   ~BatchModelRunner();
   BatchModelRunner(const BatchModelRunner &) = delete;
   BatchModelRunner &operator=(const BatchModelRunner &) = delete;

@@ -173,6 +173,9 @@ struct BatchModelRunner::Implementation {
   int probe_kind = probe_none;
   // Construction-time weight source (null: seeded weights) and its staging.
   const Checkpoint *checkpoint = nullptr;
+  // device-resident bf16 segments (the reference's DeviceWeightArena) when constructing from them
+  BatchModelRunner::DeviceSegmentFn device_segment = nullptr;
+  void *device_segment_context = nullptr;
   DeviceBuffer load_staging;
   std::unique_ptr<void, void (*)(void *)> pinned{nullptr, [](void *p) {
     if (p != nullptr) (void)hipHostFree(p);
@@ -217,12 +220,15 @@ struct BatchModelRunner::Implementation {
   int32_t *a_tokens = nullptr, *a_outputs = nullptr, *a_forced = nullptr, *a_context = nullptr,
           *a_slots = nullptr, *a_proposals = nullptr;
 
-  Implementation(const ModelSpec &model, int batch, int context, const Checkpoint *source = nullptr)
+  Implementation(const ModelSpec &model, int batch, int context, const Checkpoint *source = nullptr,
+                 BatchModelRunner::DeviceSegmentFn segment = nullptr, void *segment_context = nullptr)
       : spec(model), batch_size(batch), maximum_context(context),
         maximum_rows(batch * kMaximumDepth),
         step_rows(std::max(batch * kMaximumDepth, std::min(kPrefillStepRows, context))),
         slot_positions(static_cast<size_t>(batch), 0) {
     checkpoint = source;
+    device_segment = segment;
+    device_segment_context = segment_context;
     if (batch <= 0 || batch > 64 || context <= 0 || spec.layers.empty() || spec.hidden <= 0 ||
         spec.intermediate <= 0 || spec.vocabulary <= 0)
       throw std::runtime_error("invalid runner shape");
@@ -247,6 +253,8 @@ struct BatchModelRunner::Implementation {
     load_staging.release();
     pinned.reset();
     checkpoint = nullptr;
+    device_segment = nullptr;
+    device_segment_context = nullptr;
   }
 
   // Next probe event pair when `kind` is being probed (else a null pair).
@@ -295,11 +303,24 @@ struct BatchModelRunner::Implementation {
 
   uint64_t seed_for(uint64_t tensor) const { return spec.seed * 1000003ull + tensor * 7919ull; }
 
-  // ---- weight sources: a checkpoint segment when loading one, else seeded values. Segment
-  // names are the execution plan's ("layer.3.qkv"; "assistant." selects the assistant's plan).
+  // ---- weight sources: a checkpoint segment or a device-resident segment when loading one,
+  // else seeded values. Segment names are the execution plan's ("layer.3.qkv"; "assistant."
+  // selects the assistant's plan).
+  bool has_source() const { return checkpoint != nullptr || device_segment != nullptr; }
+
   void upload_segment(const std::string &name, void *device, size_t bytes) {
     const bool assistant = name.rfind("assistant.", 0) == 0;
     const std::string segment = assistant ? name.substr(10) : name;
+    if (device_segment != nullptr) {
+      const void *source =
+          device_segment(device_segment_context, assistant ? 1 : 0, 0, segment.c_str(), nullptr);
+      if (source == nullptr)
+        throw std::runtime_error(std::string(assistant ? "assistant" : "target") +
+                                 " device weights have no segment " + segment);
+      hip_check(hipMemcpyAsync(device, source, bytes, hipMemcpyDeviceToDevice, stream),
+                "copy device weight segment");
+      return;
+    }
     const WeightSegment &s = (assistant ? checkpoint->assistant_plan : checkpoint->target_plan).at(segment);
     if (s.bytes != bytes)
       throw std::runtime_error("checkpoint weight " + name + " has " + std::to_string(s.bytes) +
@@ -325,12 +346,31 @@ struct BatchModelRunner::Implementation {
 
   void fill_norm(DeviceBuffer &buffer, int n, uint64_t tensor, const std::string &segment) {
     buffer.allocate(sizeof(bf16_t) * static_cast<size_t>(n));
-    if (checkpoint != nullptr) {
+    if (has_source()) {
       upload_segment(segment, buffer.get(), buffer.bytes());
       return;
     }
     fill_normal_bf16(buffer.as<bf16_t>(), static_cast<size_t>(n), seed_for(tensor), 1.0f, 0.05f,
                      stream);
+  }
+
+  // The device source's own e4m3 copy of a segment (Fp8WeightArena) into `dst` and its scale
+  // into `scale`; false when the source has none (the bf16 segment is quantised instead).
+  bool copy_device_fp8(const std::string &name, void *dst, size_t bytes, float *scale) {
+    if (device_segment == nullptr) return false;
+    const bool assistant = name.rfind("assistant.", 0) == 0;
+    const std::string segment = assistant ? name.substr(10) : name;
+    const float *source_scale = nullptr;
+    const void *source = device_segment(device_segment_context, assistant ? 1 : 0, 1,
+                                        segment.c_str(), &source_scale);
+    if (source == nullptr) return false;
+    if (source_scale == nullptr)
+      throw std::runtime_error("device fp8 weight " + segment + " has no scale");
+    hip_check(hipMemcpyAsync(dst, source, bytes, hipMemcpyDeviceToDevice, stream),
+              "copy device fp8 weight segment");
+    hip_check(hipMemcpyAsync(scale, source_scale, sizeof(float), hipMemcpyDeviceToDevice, stream),
+              "copy device fp8 weight scale");
+    return true;
   }
 
   void *staging_for(size_t bytes) {
@@ -353,7 +393,9 @@ struct BatchModelRunner::Implementation {
   void fill_fp8(PackedWeight &w, int n, int k, bool gate_up, uint64_t tensor, float *scale,
                 const std::string &segment) {
     const size_t count = static_cast<size_t>(n) * k;
-    if (checkpoint != nullptr) {
+    if (copy_device_fp8(segment, staging_for(count), count, scale)) {
+      // the source's own e4m3 bytes and scale (Fp8WeightArena::quantize already ran)
+    } else if (has_source()) {
       if (load_staging.bytes() < count * sizeof(bf16_t)) {
         hip_check(hipStreamSynchronize(stream), "synchronise before staging growth");
         load_staging.release();
@@ -374,7 +416,7 @@ struct BatchModelRunner::Implementation {
                         float stddev, const std::string &segment) {
     const size_t count = static_cast<size_t>(n) * k;
     void *dst = staging_for(count * sizeof(bf16_t));
-    if (checkpoint != nullptr)
+    if (has_source())
       upload_segment(segment, dst, count * sizeof(bf16_t));
     else
       fill_normal_bf16(static_cast<bf16_t *>(dst), count, seed_for(tensor), 0.0f, stddev, stream);
@@ -384,7 +426,7 @@ struct BatchModelRunner::Implementation {
   void fill_bf16(DeviceBuffer &buffer, size_t n, uint64_t tensor, float stddev,
                  const std::string &segment) {
     buffer.allocate(sizeof(bf16_t) * n);
-    if (checkpoint != nullptr)
+    if (has_source())
       upload_segment(segment, buffer.get(), buffer.bytes());
     else
       fill_normal_bf16(buffer.as<bf16_t>(), n, seed_for(tensor), 0.0f, stddev, stream);
@@ -437,11 +479,13 @@ struct BatchModelRunner::Implementation {
     }
     fill_bf16(embedding_bf16, static_cast<size_t>(spec.vocabulary) * H, 1, 1.0f, "token_embedding");
     embedding_scale.allocate(sizeof(float));
-    quantize_weight_bf16_to_fp8(
-        embedding_bf16.as<bf16_t>(),
-        static_cast<fp8_t *>(staging_for(static_cast<size_t>(spec.vocabulary) * H)),
-        static_cast<size_t>(spec.vocabulary) * H, embedding_scale.as<float>(),
-        init_scratch.as<float>(), stream);
+    const size_t embedding_count = static_cast<size_t>(spec.vocabulary) * H;
+    if (!copy_device_fp8("token_embedding", staging_for(embedding_count), embedding_count,
+                         embedding_scale.as<float>()))
+      quantize_weight_bf16_to_fp8(embedding_bf16.as<bf16_t>(),
+                                  static_cast<fp8_t *>(staging_for(embedding_count)),
+                                  embedding_count, embedding_scale.as<float>(),
+                                  init_scratch.as<float>(), stream);
     pack_from_staging(lm_head, spec.vocabulary, spec.hidden, false);
     fill_norm(final_norm, spec.hidden, 2, "final_norm");
     upload_rope();
@@ -1704,6 +1748,13 @@ ModelSpec spec_of(const Checkpoint &checkpoint) {
 BatchModelRunner::BatchModelRunner(const Checkpoint &checkpoint, int batch, int maximum_context)
     : implementation_(std::make_unique<Implementation>(spec_of(checkpoint), batch, maximum_context,
                                                        &checkpoint)) {}
+
+BatchModelRunner::BatchModelRunner(const ModelSpec &spec, DeviceSegmentFn segment, void *context,
+                                   int batch, int maximum_context)
+    : implementation_(std::make_unique<Implementation>(
+          spec, batch, maximum_context, nullptr,
+          segment != nullptr ? segment : throw std::runtime_error("missing device weight lookup"),
+          context)) {}
 
 BatchModelRunner::BatchModelRunner(const ModelSpec &spec, int batch, int maximum_context)
     : implementation_(std::make_unique<Implementation>(spec, batch, maximum_context)) {}

@@ -134,6 +134,39 @@ class BatchModelRunner:
         self.last_predictions = []
         return self
 
+    SEGMENT_FN = ctypes.CFUNCTYPE(ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                  ctypes.c_char_p, ctypes.POINTER(ctypes.c_void_p))
+
+    @classmethod
+    def from_device_weights(cls, desc: ModelDesc, segments: dict, batch: int, maximum_context: int,
+                            fp8_segments: dict | None = None) -> "BatchModelRunner":
+        """The runner over weights already on the device (DeviceWeightArena / Fp8WeightArena,
+        device_weights.h:15-52). `segments` maps (assistant, name) to the device address of the
+        bf16 execution segment the reference's WeightPlan calls `name`; `fp8_segments` (optional)
+        maps it to (e4m3 segment address, device address of its fp32 scale)."""
+        fp8_segments = fp8_segments or {}
+
+        def lookup(_context, assistant, fp8, name, scale):
+            key = (bool(assistant), name.decode())
+            if fp8:
+                entry = fp8_segments.get(key)
+                if entry is None:
+                    return None
+                scale[0] = entry[1]
+                return entry[0]
+            return segments.get(key)
+
+        callback = cls.SEGMENT_FN(lookup)
+        self = cls.__new__(cls)
+        self._desc = desc
+        c_desc, self._layers_keepalive = desc.to_c()
+        handle = ctypes.c_void_p()
+        check(lib().carat_hip_runner_create_from_device_weights(
+            ctypes.byref(c_desc), callback, None, batch, maximum_context, ctypes.byref(handle)))
+        self._handle = handle
+        self.last_predictions = []
+        return self
+
     def close(self) -> None:
         if getattr(self, "_handle", None):
             lib().carat_hip_runner_destroy(self._handle)

@@ -102,6 +102,22 @@ int carat_hip_checkpoint_describe(const char *model_dir, const char *assistant_d
 int carat_hip_runner_create_from_checkpoint(const char *model_dir, const char *assistant_dir,
                                             int batch, int maximum_context,
                                             carat_hip_runner **out);
+/* Gemma4BatchModelRunner(config, weights, batch, maximum_context, fp8, assistant, assistant_fp8)
+ * (batch_model_runner.h:24-28) over weights already resident on the device (DeviceWeightArena /
+ * Fp8WeightArena, include/carat/device_weights.h:15-52): segment(context, assistant, fp8, name,
+ * &scale) returns the device address of the execution segment the reference's WeightPlan names
+ * `name` ("token_embedding", "layer.3.qkv", ...; weight_plan.cpp:37-189; assistant = 1 selects
+ * the assistant's plan) -- bf16 when fp8 == 0; when fp8 == 1 its e4m3 copy with the per-tensor
+ * scale's device address stored to *scale, or NULL, and the runner then quantises the bf16
+ * segment per tensor (amax/448) itself. Segments are copied device to device during
+ * construction (the arenas may be freed afterwards) and packed. desc gives the shapes; its seed
+ * and weight_std are unused. */
+typedef const void *(*carat_hip_device_segment_fn)(void *context, int assistant, int fp8,
+                                                   const char *name, const float **scale);
+int carat_hip_runner_create_from_device_weights(const carat_hip_model_desc *desc,
+                                                carat_hip_device_segment_fn segment,
+                                                void *context, int batch, int maximum_context,
+                                                carat_hip_runner **out);
 void carat_hip_runner_destroy(carat_hip_runner *runner);
 /* Test/benchmark helper, no counterpart in the reference: the target predictions (argmax of every
  * row, [rows]) of the last verify, append or prefill step; *count = rows (min(rows, capacity)

@@ -1,71 +1,35 @@
-// C++ drop-in for the reference's runner and speculation interfaces, header-only over the C ABI
-// in carat_hip.h. Class, method and type names, argument meaning and error behaviour follow
-// include/carat/batch_model_runner.h:10-77 and src/runtime/speculation.h:11-27 of the reference:
+// C++ drop-in for the reference's runner interface, header-only over the C ABI in carat_hip.h
+// (the speculation helpers are in carat_hip_speculation.hpp). Class, method and type names,
+// argument meaning and error behaviour follow include/carat/batch_model_runner.h:10-77 of the
+// reference:
 // every failure is rethrown as std::runtime_error carrying the library's message, which is the
 // reference's own text (batch_model_runner.cu:1006-1810), so CHECK_THROWS(expr, fragment) style
 // tests keep working. The reference's serving loop (native_runtime_main.cpp:583-678) calls these
 // unchanged.
 //
-// Construction differs where the reference passes CUDA weight arenas: a runner is built from a
-// Gemma-4 checkpoint directory (config.json + safetensors, weights quantised and packed on the
-// device) or from a carat_hip_model_desc of seeded synthetic weights.
+// Construction: the reference's own constructor (config + device weight arenas) is declared here
+// and defined in carat_amd/binding/batch_model_runner_binding.cpp, which compiles against the
+// reference's Gemma4Config / DeviceWeightArena / Fp8WeightArena headers. A runner can also be
+// built from a Gemma-4 checkpoint directory (config.json + safetensors, weights quantised and
+// packed on the device) or from a carat_hip_model_desc of seeded synthetic weights.
 #pragma once
 
 #include "carat_hip.h"
 
 #include <cstdint>
 #include <optional>
-#include <span>
 #include <stdexcept>
 #include <string>
-#include <unordered_set>
 #include <vector>
 
 namespace carat {
 
+struct Gemma4Config;
+class DeviceWeightArena;
+class Fp8WeightArena;
+
 inline void hip_ok(int status) {
   if (status != 0) throw std::runtime_error(carat_hip_last_error());
-}
-
-// ------------------------------------------------------------------ speculation.h:11-27
-[[nodiscard]] inline int acceptance_cap(int depth, int remaining, std::span<const int> proposals,
-                                        const std::unordered_set<int> &stop_ids) {
-  const std::vector<int32_t> stops(stop_ids.begin(), stop_ids.end());
-  int cap = 0;
-  hip_ok(carat_hip_acceptance_cap(depth, remaining, proposals.data(),
-                                  static_cast<int>(proposals.size()), stops.data(),
-                                  static_cast<int>(stops.size()), &cap));
-  return cap;
-}
-
-struct SpeculativeCommit {
-  std::vector<int> resident_tokens;
-  std::vector<int> emitted_tokens;
-  int next_token{0};
-  bool stopped{false};
-};
-
-[[nodiscard]] inline SpeculativeCommit commit_speculation(int forced_token,
-                                                          std::span<const int> accepted_drafts,
-                                                          int next_token,
-                                                          const std::unordered_set<int> &stop_ids) {
-  const std::vector<int32_t> stops(stop_ids.begin(), stop_ids.end());
-  const size_t n = accepted_drafts.size() + 1;
-  SpeculativeCommit out;
-  out.resident_tokens.resize(n);
-  out.emitted_tokens.resize(n);
-  int resident = 0, emitted = 0, stopped = 0;
-  int32_t next = 0;
-  hip_ok(carat_hip_commit_speculation(forced_token, accepted_drafts.data(),
-                                      static_cast<int>(accepted_drafts.size()), next_token,
-                                      stops.data(), static_cast<int>(stops.size()),
-                                      out.resident_tokens.data(), &resident,
-                                      out.emitted_tokens.data(), &emitted, &next, &stopped));
-  out.resident_tokens.resize(static_cast<size_t>(resident));
-  out.emitted_tokens.resize(static_cast<size_t>(emitted));
-  out.next_token = next;
-  out.stopped = stopped != 0;
-  return out;
 }
 
 // ------------------------------------------------------------------ batch_model_runner.h:10-77
@@ -81,6 +45,13 @@ struct LayerSlicedSuffixPrefillResult {
 
 class Gemma4BatchModelRunner {
 public:
+  // batch_model_runner.h:24-28. Defined in carat_amd/binding/batch_model_runner_binding.cpp
+  // (built with the reference's headers): the arenas' bf16 segments, and the FP8 arena's e4m3
+  // segments and scales when given, are copied into the runner during construction.
+  Gemma4BatchModelRunner(const Gemma4Config &config, const DeviceWeightArena &weights, int batch,
+                         int maximum_context, const Fp8WeightArena *fp8_weights = nullptr,
+                         const DeviceWeightArena *assistant_weights = nullptr,
+                         const Fp8WeightArena *assistant_fp8_weights = nullptr);
   // Seeded synthetic weights of the described shape.
   Gemma4BatchModelRunner(const carat_hip_model_desc &desc, int batch, int maximum_context) {
     hip_ok(carat_hip_runner_create(&desc, batch, maximum_context, &runner_));

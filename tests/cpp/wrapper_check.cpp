@@ -6,6 +6,7 @@
 //   wrapper_check runner         a tiny synthetic model on the GPU: prefill, clone, draft,
 //                                verify, append_ragged, and the reference's error texts
 #include "carat_hip_runner.hpp"
+#include "carat_hip_speculation.hpp"
 
 #include <cstdio>
 #include <fstream>

@@ -115,3 +115,102 @@ def test_verify_step_over_checkpoint_weights(loaded):
     assert np.all(gap <= 0.05 * logits.std())
     drafts = runner.draft_four(first.tolist(), slots, first.tolist(), 4)
     assert [row[0] for row in drafts] == first.tolist()
+
+
+def plan_segments(cfg, tensors, a_tensors):
+    """Execution segments of the reference's WeightPlan::gemma4 / gemma4_assistant
+    (weight_plan.cpp:37-127) built from the checkpoint tensors: {(assistant, name): bf16 array}."""
+    t = cfg["text_config"]
+    out = {(False, "token_embedding"): tensors["model.language_model.embed_tokens.weight"],
+           (False, "final_norm"): tensors["model.language_model.norm.weight"]}
+    single = {"input_norm": "input_layernorm.weight", "q_norm": "self_attn.q_norm.weight",
+              "k_norm": "self_attn.k_norm.weight", "o": "self_attn.o_proj.weight",
+              "post_attention_norm": "post_attention_layernorm.weight",
+              "pre_mlp_norm": "pre_feedforward_layernorm.weight", "down": "mlp.down_proj.weight",
+              "post_mlp_norm": "post_feedforward_layernorm.weight", "scalar": "layer_scalar"}
+    for li, kind in enumerate(t["layer_types"]):
+        p = f"model.language_model.layers.{li}."
+        for name, src in single.items():
+            out[(False, f"layer.{li}.{name}")] = tensors[p + src]
+        parts = [tensors[p + "self_attn.q_proj.weight"], tensors[p + "self_attn.k_proj.weight"]]
+        if kind == "sliding_attention":
+            parts.append(tensors[p + "self_attn.v_proj.weight"])
+        out[(False, f"layer.{li}.qkv")] = np.concatenate(parts)
+        out[(False, f"layer.{li}.gate_up")] = np.concatenate(
+            [tensors[p + "mlp.gate_proj.weight"], tensors[p + "mlp.up_proj.weight"]])
+    out.update({(True, "token_embedding"): a_tensors["model.embed_tokens.weight"],
+                (True, "pre_projection"): a_tensors["pre_projection.weight"],
+                (True, "post_projection"): a_tensors["post_projection.weight"],
+                (True, "final_norm"): a_tensors["model.norm.weight"]})
+    a_single = dict(single, q="self_attn.q_proj.weight")
+    del a_single["k_norm"]
+    li = 0
+    while f"model.layers.{li}.input_layernorm.weight" in a_tensors:
+        p = f"model.layers.{li}."
+        for name, src in a_single.items():
+            out[(True, f"layer.{li}.{name}")] = a_tensors[p + src]
+        out[(True, f"layer.{li}.gate_up")] = np.concatenate(
+            [a_tensors[p + "mlp.gate_proj.weight"], a_tensors[p + "mlp.up_proj.weight"]])
+        li += 1
+    return out
+
+
+def test_runner_from_device_weights_equals_checkpoint_runner(loaded, torch_cuda):
+    """Gemma4BatchModelRunner(config, DeviceWeightArena, ..., Fp8WeightArena) over device-resident
+    plan segments: with bf16 segments only, every weight and a verify step equal the checkpoint
+    runner's bit for bit; with the arena's own e4m3 segments and scales (here: the oracle's
+    quantisation at twice the scale, as a weight_scale_multiplier of 2 gives), those are used."""
+    torch = torch_cuda
+    runner, cfg, tensors, a_tensors = loaded
+    desc = runner._desc
+    host = plan_segments(cfg, tensors, a_tensors)
+    dev = {k: torch.from_numpy(np.ascontiguousarray(v).view(np.int16)).cuda() for k, v in host.items()}
+    addresses = {k: v.data_ptr() for k, v in dev.items()}
+    say("case: runner from device-resident bf16 segments")
+    other = BatchModelRunner.from_device_weights(desc, addresses, BATCH, MAX_CONTEXT)
+    try:
+        names = ["token_embedding", "token_embedding.fp8", "token_embedding.scale", "final_norm",
+                 "assistant.token_embedding", "assistant.layer.0.gate_up"]
+        for li in range(len(desc.layers)):
+            names += [f"layer.{li}.{n}" for n in ("qkv", "o", "gate_up", "down", "scales", "q_norm")]
+        for name in names:
+            assert np.array_equal(other.read(name, np.uint8), runner.read(name, np.uint8)), name
+        for r in (runner, other):
+            r.seed_random_cache(60, seed=22, stddev=1 / math.sqrt(128))
+        props = np.random.default_rng(9).integers(0, desc.vocabulary, (4, 5)).tolist()
+        first = [p[0] for p in props]
+        a = runner.verify_greedy_proposals(props, first, [0, 1, 2, 3], [0] * 4)
+        pa = list(runner.last_predictions)
+        b = other.verify_greedy_proposals(props, first, [0, 1, 2, 3], [0] * 4)
+        assert a == b and other.last_predictions == pa
+    finally:
+        other.close()
+    say("case: runner from device-resident e4m3 segments with their own scales")
+    fp8 = {}
+    keep = []
+    for (assistant, name), m in host.items():
+        if assistant or not (name == "token_embedding" or name.split(".")[-1] in ("qkv", "o", "gate_up", "down")):
+            continue
+        amax = float(np.abs(oracle.bf16_to_f32(m)).max())
+        q, s = oracle.quantize_e4m3(m, amax * 2.0)
+        dq = torch.from_numpy(np.ascontiguousarray(q)).cuda()
+        ds = torch.tensor([s], dtype=torch.float32, device="cuda")
+        keep += [dq, ds]
+        fp8[(False, name)] = (dq.data_ptr(), ds.data_ptr(), q, s)
+    other = BatchModelRunner.from_device_weights(desc, addresses, BATCH, MAX_CONTEXT,
+                                                 {k: v[:2] for k, v in fp8.items()})
+    try:
+        q, s = fp8[(False, "token_embedding")][2:]
+        assert np.array_equal(other.read("token_embedding.fp8", np.uint8), q.reshape(-1))
+        assert other.read("token_embedding.scale", np.float32)[0] == np.float32(s)
+        for li in range(len(desc.layers)):
+            scales = other.read(f"layer.{li}.scales", np.float32)
+            for j, n in enumerate(("qkv", "o", "gate_up", "down")):
+                q, s = fp8[(False, f"layer.{li}.{n}")][2:]
+                assert np.array_equal(other.read(f"layer.{li}.{n}", np.uint8), q.reshape(-1)), (li, n)
+                assert scales[j] == np.float32(s)
+    finally:
+        other.close()
+    with pytest.raises(Exception, match="device weights have no segment final_norm"):
+        BatchModelRunner.from_device_weights(
+            desc, {k: v for k, v in addresses.items() if k != (False, "final_norm")}, BATCH, MAX_CONTEXT)
