@@ -53,7 +53,8 @@ struct AttentionArgs {
 
 size_t attention_partials_floats(int requests, int kv_heads, int max_keys, int chunk_keys,
                                  int query_rows, int dimension);
-int attention_default_chunk(AttentionMode mode, int max_keys, int requests, int kv_heads);
+int attention_default_chunk(AttentionMode mode, int max_keys, int requests, int kv_heads,
+                            bool fp8_kv = false, int dimension = 128);
 void launch_attention(const AttentionArgs &args, hipStream_t stream);
 
 }  // namespace carat_hip

@@ -983,16 +983,25 @@ size_t attention_partials_floats(int requests, int kv_heads, int max_keys, int c
 }
 
 
-int attention_default_chunk(AttentionMode mode, int max_keys, int requests, int kv_heads) {
+int attention_default_chunk(AttentionMode mode, int max_keys, int requests, int kv_heads,
+                            bool fp8_kv, int dimension) {
   // One workgroup per (request, kv head) streams the whole key range when that already gives
   // >= 256 workgroups: two or three co-reside per CU, so an uneven count still shares the HBM
   // stream evenly, and no partials or merge kernel are needed (measured on MI355X, 24 slots x 16
   // kv heads: global verify 290 us in one chunk, 287 us in four 2048-key chunks plus the merge;
   // sliding verify 50 us whole, 54 us in two chunks plus the merge). Smaller batches split the
   // range so that up to 512 workgroups stream it.
-  (void)mode;
+  //
+  // e4m3 K/V at D = 128 is the exception: a workgroup moves half the bytes per key, and with one
+  // workgroup per pair the 128 CUs holding two of them fall behind the 128 holding one (cold
+  // HBM, 24 x 16 pairs x 8155 keys: the single-workgroup CUs finish 134 us in, the last
+  // workgroups at 182 us). Two chunks per pair put exactly three workgroups on every CU
+  // (768 workgroups at three per CU): 152 us plus the merge.
   const int whole = ((max_keys + 255) / 256) * 256;
   const int pairs = std::max(1, requests * kv_heads);
+  if (fp8_kv && mode != AttentionMode::decode && dimension == 128 && pairs >= 256 &&
+      2 * pairs <= 3 * 256 && max_keys >= 2048)
+    return ((max_keys + 1) / 2 + 255) / 256 * 256;
   if (pairs >= 256) return whole;
   // the smallest 256-key multiple that keeps the workgroups at <= 512
   const long chunks = std::max(1L, 512L / pairs);

@@ -755,7 +755,8 @@ int carat_hip_verify_attention(int mode, const uint16_t *q, const void *k_cache,
     a.out = out;
     a.out_amax = out_amax;
     a.chunk_keys = chunk_keys > 0 ? chunk_keys
-                                  : attention_default_chunk(a.mode, max_keys, requests, kv_heads);
+                                  : attention_default_chunk(a.mode, max_keys, requests, kv_heads, a.fp8_kv,
+                                                            dimension);
     std::lock_guard<std::mutex> lock(workspace_mutex);
     OpWorkspace &w = workspace_for_current_device();
     if (kv_heads <= 0 || requests <= 0 || max_keys <= 0)

@@ -629,6 +629,14 @@ WeightLayout gemm_weight_layout(int n, int row_bytes, bool gate_up) {
   const int unit = 16 * l.tiles_per_wave;  // rows per wave
   if (gate_up && n / (4 * unit) < 192 && n % (3 * unit) == 0 && n / (3 * unit) <= 256)
     l.waves = 3;
+  // Split-K layouts: 3-wave blocks when 4-wave ones leave CUs idle after the split (o 5376 x
+  // 4096: 224 workgroups instead of 168).
+  if (!gate_up && l.tiles_per_wave == 1 && n % 48 == 0) {
+    const int steps = row_bytes / 128;
+    const int wg4 = (n / 64) * gemm_choose_splits(n / 64, steps);
+    const int wg3 = (n / 48) * gemm_choose_splits(n / 48, steps);
+    if (wg4 < 200 && wg3 > wg4 && wg3 <= 256) l.waves = 3;
+  }
   check_layout(l);
   return l;
 }

@@ -71,7 +71,7 @@ def test_gemm_plan_is_the_runner_dispatch():
         return f.value, w.value, s.value
 
     assert plan(8192, 5376, 1, 0) == (1, 4, 2)       # qkv
-    assert plan(5376, 4096, 1, 0) == (1, 4, 2)       # o
+    assert plan(5376, 4096, 1, 0) == (1, 3, 2)       # o (3-wave blocks: 224 workgroups)
     assert plan(43008, 5376, 1, 1) == (4, 3, 1)      # gate/up (GELU epilogue: no split-K)
     assert plan(5376, 21504, 1, 0) == (1, 4, 3)      # down
     assert plan(262144, 5376, 1, 0) == (4, 4, 1)     # lm_head

@@ -63,7 +63,7 @@ def plan(n, k, gate_up):
 
 # name, n, k, gate_up, the runner's (tiles per wave, waves, splits) for that weight
 CONFIG4 = [("qkv", (32 + 2 * 16) * 128, H, False, (1, 4, 2)),
-           ("o", H, 32 * 128, False, (1, 4, 2)),
+           ("o", H, 32 * 128, False, (1, 3, 2)),
            ("gate_up", 2 * INTER, H, True, (4, 3, 1)),
            ("down", H, INTER, False, (1, 4, 3)),
            ("lm_head", VOCAB, H, False, (4, 4, 1))]
