@@ -94,16 +94,36 @@ __device__ __forceinline__ float fp8_scale_from_amax(float amax) {
 // wave / block reductions (wave64)
 // ---------------------------------------------------------------------------------------------
 
+// Wave64 reductions on the DPP network (VALU lane moves, no LDS round trip per step): butterflies
+// inside each quad and row of 16 lanes, then the row totals are carried up with row broadcasts
+// into lane 63, whose value every lane receives. DPP controls (GFX9): quad_perm(1,0,3,2) = 0xB1,
+// quad_perm(2,3,0,1) = 0x4E, row_half_mirror = 0x141, row_mirror = 0x140, row_bcast15 = 0x142,
+// row_bcast31 = 0x143.
+template <int kCtrl, int kRowMask = 0xF>
+__device__ __forceinline__ float dpp_move(float old, float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, old),
+                                                              __builtin_bit_cast(int, v), kCtrl,
+                                                              kRowMask, 0xF, false));
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int offset = 32; offset > 0; offset >>= 1) v += __shfl_xor(v, offset, kWave);
-  return v;
+  v += dpp_move<0xB1>(0.0f, v);
+  v += dpp_move<0x4E>(0.0f, v);
+  v += dpp_move<0x141>(0.0f, v);
+  v += dpp_move<0x140>(0.0f, v);       // every lane: its row's sum
+  v += dpp_move<0x142, 0xA>(0.0f, v);  // rows 1, 3 += rows 0, 2
+  v += dpp_move<0x143, 0xC>(0.0f, v);  // row 3 += rows 0 + 1
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int offset = 32; offset > 0; offset >>= 1) v = fmaxf(v, __shfl_xor(v, offset, kWave));
-  return v;
+  v = fmaxf(v, dpp_move<0xB1>(v, v));
+  v = fmaxf(v, dpp_move<0x4E>(v, v));
+  v = fmaxf(v, dpp_move<0x141>(v, v));
+  v = fmaxf(v, dpp_move<0x140>(v, v));
+  v = fmaxf(v, dpp_move<0x142, 0xA>(v, v));
+  v = fmaxf(v, dpp_move<0x143, 0xC>(v, v));
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
 // Block-wide sum; `scratch` needs blockDim.x / 64 floats. All threads get the result.

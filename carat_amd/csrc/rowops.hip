@@ -4,6 +4,7 @@
 #include "rowops.h"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace carat_hip {
 namespace {
@@ -144,9 +145,92 @@ __global__ __launch_bounds__(kThreads) void row_kernel(const RowArgs a) {
   }
 }
 
+// The verify step's layer-end rows, with every option fixed at compile time: split-K partials
+// (kSplits of them, fp8 output scale), stage 1 with residual (layer scalar optional, a uniform
+// load), stage 2 with amax. One workgroup per row, kThreads threads of Q quads each (width 5376:
+// 448 threads x 3 quads, no idle lanes). Every global load of the row is issued in one straight
+// run before the first reduction (no conditional load: the layer scalar's address is selected,
+// not branched on); the runtime options of row_kernel put waits between them.
+template <int Q, int kThreads, int kSplits>
+__global__ __launch_bounds__(kThreads) void layer_end_kernel(const RowArgs a) {
+  constexpr int kWaves = kThreads / kWave;
+  __shared__ float scratch[kWaves];
+  const int row = blockIdx.x;
+  const int quads = a.width / 4;
+  const size_t row_offset = static_cast<size_t>(row) * a.width;
+  const float w_scale = *a.w_scale;
+  const float layer_scalar = bf16_to_f32(*(a.scalar != nullptr ? a.scalar : a.w2));
+  f32x4_t v[Q], w1[Q], res[Q], w2[Q];
+  f32x4_t part[Q][kSplits];
+#pragma unroll
+  for (int i = 0; i < Q; ++i) {
+    const int q = min(threadIdx.x + i * kThreads, quads - 1);  // tail lanes re-read the last quad
+#pragma unroll
+    for (int k = 0; k < kSplits; ++k)
+      part[i][k] = reinterpret_cast<const f32x4_t *>(a.partials + (static_cast<size_t>(k) * a.rows + row) * a.width)[q];
+    w1[i] = bf16x4_to_f32(reinterpret_cast<const uint2 *>(a.w1)[q]);
+    res[i] = bf16x4_to_f32(reinterpret_cast<const uint2 *>(a.residual + row_offset)[q]);
+    w2[i] = bf16x4_to_f32(reinterpret_cast<const uint2 *>(a.w2)[q]);
+  }
+  const float amax_part = amax_lane(a.x_amax, a.amax_stripes);
+  const float scale = w_scale * fp8_scale_from_amax(wave_max(amax_part));
+
+  float square_sum = 0.0f;
+#pragma unroll
+  for (int i = 0; i < Q; ++i) {
+    const bool live = threadIdx.x + i * kThreads < quads;
+    f32x4_t sum = part[i][0];
+#pragma unroll
+    for (int k = 1; k < kSplits; ++k) sum += part[i][k];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      v[i][c] = live ? round_bf16(sum[c] * scale) : 0.0f;
+      square_sum += v[i][c] * v[i][c];
+    }
+  }
+
+  // stage 1: r1 = bf16(norm(v) * w1 + residual) [* scalar]
+  const bool has_scalar = a.scalar != nullptr;
+  float inv = inverse_rms(block_sum(square_sum, scratch), a.width, a.eps);
+  square_sum = 0.0f;
+#pragma unroll
+  for (int i = 0; i < Q; ++i) {
+    const int q = threadIdx.x + i * kThreads;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      float r1 = round_bf16(v[i][c] * inv * w1[i][c] + res[i][c]);
+      if (has_scalar) r1 = round_bf16(r1 * layer_scalar);
+      v[i][c] = q < quads ? r1 : 0.0f;
+      square_sum += v[i][c] * v[i][c];
+    }
+    if (q < quads) reinterpret_cast<uint2 *>(a.r1_out + row_offset)[q] = f32x4_to_bf16(v[i]);
+  }
+
+  // stage 2: y = bf16(norm(r1) * w2), amax
+  inv = inverse_rms(block_sum(square_sum, scratch), a.width, a.eps);
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < Q; ++i) {
+    const int q = threadIdx.x + i * kThreads;
+    f32x4_t y;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      y[c] = round_bf16(v[i][c] * inv * w2[i][c]);
+      amax = fmaxf(amax, fabsf(y[c]));
+    }
+    if (q < quads) reinterpret_cast<uint2 *>(a.y_out + row_offset)[q] = f32x4_to_bf16(y);
+  }
+  amax = block_max(amax, scratch);
+  if (threadIdx.x == 0) amax_publish(a.y_amax, a.amax_stripes, amax);
+}
+
 // One wave per (row, head). Lane l owns elements [l*E, l*E+E) with E = D/64; the rotate-half
-// partner of element i (i +- D/2) lives in lane l ^ 32.
-template <int D>
+// partner of element i (i +- D/2) lives in lane l ^ 32. kSplits > 0: the source is that many
+// split-K partials (a compile-time count, so that every load of the wave -- partials, scale
+// operands, norm weight, position -- goes out in one straight run, and only the RoPE table rows,
+// which need the position, wait for it); kSplits = 0: the packed bf16 rows or any other split
+// count.
+template <int D, int kSplits>
 __global__ __launch_bounds__(64) void qkv_post_kernel(const QkvArgs a) {
   constexpr int E = D / 64;
   const int row = blockIdx.x;
@@ -175,42 +259,76 @@ __global__ __launch_bounds__(64) void qkv_post_kernel(const QkvArgs a) {
     column0 = query_width + kv_width + h * D;
   }
 
-  // Every independent load is issued before the first use: the scale operands, the position,
-  // and the split-K partials (up to kQkvUnrolledSplits of them without a dependent chain).
   const int request = row / a.tokens;
   const int t = row % a.tokens;
   const int position_base = a.positions[request];
-  float amax_part = 0.0f, w_scale = 1.0f;
-  if (a.x_amax != nullptr) amax_part = amax_lane(a.x_amax, a.amax_stripes);
-  if (a.w_scale != nullptr) w_scale = *a.w_scale;
+  // the norm weight of this head's kind (the V rows have none; they load q_norm unused)
+  const bf16_t *norm_w = kind == 1 ? a.k_norm : a.q_norm;
+  const int c0 = column0 + lane * E;
   float raw[E];
+  float amax_part = 0.0f, w_scale = 1.0f;
+  float part[kSplits > 0 ? kSplits : 1][E];
+  if constexpr (kSplits > 0) {
 #pragma unroll
-  for (int e = 0; e < E; ++e) {
-    const int c = column0 + lane * E + e;
-    if (a.partials != nullptr) {
-      float part[kQkvUnrolledSplits];
+    for (int k = 0; k < kSplits; ++k)
 #pragma unroll
-      for (int k = 0; k < kQkvUnrolledSplits; ++k)
-        part[k] = a.partials[(static_cast<size_t>(min(k, a.splits - 1)) * a.rows + row) * packed_width + c];
-      float sum = part[0];
+      for (int e = 0; e < E; ++e)
+        part[k][e] = a.partials[(static_cast<size_t>(k) * a.rows + row) * packed_width + c0 + e];
+    amax_part = amax_lane(a.x_amax, a.amax_stripes);
+    w_scale = *a.w_scale;
+  } else {
+    if (a.x_amax != nullptr) amax_part = amax_lane(a.x_amax, a.amax_stripes);
+    if (a.w_scale != nullptr) w_scale = *a.w_scale;
 #pragma unroll
-      for (int k = 1; k < kQkvUnrolledSplits; ++k) sum += k < a.splits ? part[k] : 0.0f;
-      for (int k = kQkvUnrolledSplits; k < a.splits; ++k)
-        sum += a.partials[(static_cast<size_t>(k) * a.rows + row) * packed_width + c];
+    for (int e = 0; e < E; ++e) {
+      const int c = c0 + e;
+      if (a.partials != nullptr) {
+        float part[kQkvUnrolledSplits];
+#pragma unroll
+        for (int k = 0; k < kQkvUnrolledSplits; ++k)
+          part[k] = a.partials[(static_cast<size_t>(min(k, a.splits - 1)) * a.rows + row) * packed_width + c];
+        float sum = part[0];
+#pragma unroll
+        for (int k = 1; k < kQkvUnrolledSplits; ++k) sum += k < a.splits ? part[k] : 0.0f;
+        for (int k = kQkvUnrolledSplits; k < a.splits; ++k)
+          sum += a.partials[(static_cast<size_t>(k) * a.rows + row) * packed_width + c];
+        raw[e] = sum;
+      } else {
+        raw[e] = bf16_to_f32(a.packed[static_cast<size_t>(row) * packed_width + c]);
+      }
+    }
+  }
+  float wv[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) wv[e] = bf16_to_f32(norm_w[lane * E + e]);
+  // every independent load above is issued before the RoPE rows wait for the position
+  __asm__ volatile("" ::: "memory");
+  if constexpr (kSplits > 0) {
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      float sum = part[0][e];
+#pragma unroll
+      for (int k = 1; k < kSplits; ++k) sum += part[k][e];
       raw[e] = sum;
-    } else {
-      raw[e] = bf16_to_f32(a.packed[static_cast<size_t>(row) * packed_width + c]);
     }
   }
   const int position = position_base + t + a.position_offset;
+  // the RoPE rows of this position: the only loads that wait for another (the position)
+  float cs[E], sn[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    cs[e] = bf16_to_f32(a.cosine[static_cast<size_t>(position) * D + lane * E + e]);
+    sn[e] = bf16_to_f32(a.sine[static_cast<size_t>(position) * D + lane * E + e]);
+  }
+  const bool scaled = kSplits > 0 || a.partials != nullptr;
   float scale = w_scale;
-  if (a.x_amax != nullptr) scale *= fp8_scale_from_amax(wave_max(amax_part));
+  if (kSplits > 0 || a.x_amax != nullptr) scale *= fp8_scale_from_amax(wave_max(amax_part));
 
   float x[E];
   float square_sum = 0.0f;
 #pragma unroll
   for (int e = 0; e < E; ++e) {
-    const float v = a.partials != nullptr ? round_bf16(raw[e] * scale) : raw[e];
+    const float v = scaled ? round_bf16(raw[e] * scale) : raw[e];
     x[e] = v;
     square_sum += v * v;
   }
@@ -230,19 +348,16 @@ __global__ __launch_bounds__(64) void qkv_post_kernel(const QkvArgs a) {
   };
 
   if (kind == 0 || kind == 1) {
-    const bf16_t *w = kind == 0 ? a.q_norm : a.k_norm;
     float normalized[E];
 #pragma unroll
-    for (int e = 0; e < E; ++e) normalized[e] = round_bf16(x[e] * inv * bf16_to_f32(w[lane * E + e]));
+    for (int e = 0; e < E; ++e) normalized[e] = round_bf16(x[e] * inv * wv[e]);
     bf16_t out[E];
 #pragma unroll
     for (int e = 0; e < E; ++e) {
       const int i = lane * E + e;
       const float partner = __shfl_xor(normalized[e], 32, kWave);
       const float rotated = i < D / 2 ? -partner : partner;
-      const float c = bf16_to_f32(a.cosine[static_cast<size_t>(position) * D + i]);
-      const float s = bf16_to_f32(a.sine[static_cast<size_t>(position) * D + i]);
-      out[e] = f32_to_bf16(normalized[e] * c + rotated * s);
+      out[e] = f32_to_bf16(normalized[e] * cs[e] + rotated * sn[e]);
     }
     if (kind == 0) {
 #pragma unroll
@@ -453,11 +568,33 @@ __global__ __launch_bounds__(256) void argmax_accept_final_kernel(const ArgmaxAc
 
 }  // namespace
 
+namespace {
+// The layer-end shape of the verify step (see layer_end_kernel); false when it does not apply.
+bool launch_layer_end(const RowArgs &a, hipStream_t stream) {
+  const bool fixed = a.source == RowSource::partials && a.x_amax != nullptr &&
+                     a.w_scale != nullptr && a.w1 != nullptr && a.residual != nullptr &&
+                     a.r1_out != nullptr && a.w2 != nullptr && a.y_out != nullptr &&
+                     a.y_amax != nullptr && a.v_out == nullptr && a.rows < 512;
+  if (!fixed || a.width != 5376 || a.splits < 1 || a.splits > 4) return false;
+  switch (a.splits) {
+  case 1: layer_end_kernel<3, 448, 1><<<a.rows, 448, 0, stream>>>(a); break;
+  case 2: layer_end_kernel<3, 448, 2><<<a.rows, 448, 0, stream>>>(a); break;
+  case 3: layer_end_kernel<3, 448, 3><<<a.rows, 448, 0, stream>>>(a); break;
+  default: layer_end_kernel<3, 448, 4><<<a.rows, 448, 0, stream>>>(a); break;
+  }
+  return true;
+}
+}  // namespace
+
 void launch_row_kernel(const RowArgs &a, hipStream_t stream) {
   if (a.rows <= 0 || a.width <= 0) throw std::runtime_error("invalid row kernel shape");
   check_amax_stripes(a.amax_stripes);
   if (a.w2 != nullptr && a.y_out == nullptr) throw std::runtime_error("row kernel: y_out missing");
   if (a.width % 4 != 0) throw std::runtime_error("row kernel: width must be a multiple of 4");
+  if (launch_layer_end(a, stream)) {
+    hip_check(hipGetLastError(), "launch row kernel");
+    return;
+  }
   const int per_thread = (a.width / 4 + kRowThreads - 1) / kRowThreads;
   if (per_thread > kRowMaxQuadsPerThread) throw std::runtime_error("row kernel: row too wide");
   // Many rows (prefill steps): 512-thread workgroups, four per CU, so that about a thousand rows
@@ -490,14 +627,31 @@ void launch_qkv_post(const QkvArgs &a, hipStream_t stream) {
   check_amax_stripes(a.amax_stripes);
   if (a.kv_heads > 0 && (a.k_new == nullptr || a.v_new == nullptr))
     throw std::runtime_error("QKV post-processing needs K/V outputs");
+  if (a.q_norm == nullptr || (a.kv_heads > 0 && a.k_norm == nullptr))
+    throw std::runtime_error("QKV post-processing needs the query and key norm weights");
   if ((a.k_cache != nullptr || a.v_cache != nullptr) && (a.slots == nullptr || a.capacity <= 0))
     throw std::runtime_error("QKV cache writes need slots and capacity");
   const int heads = a.query_heads + (a.kv_heads == 0 ? 0 : a.kv_heads * (a.key_equals_value ? 1 : 2));
   const dim3 grid(a.rows, heads);
+  // compile-time split counts for the projections' partials (1..4), else the generic path
+  const int ks = a.partials != nullptr && a.x_amax != nullptr && a.w_scale != nullptr &&
+                         a.splits >= 1 && a.splits <= 4
+                     ? a.splits
+                     : 0;
+  auto launch = [&](auto dim) {
+    constexpr int D = decltype(dim)::value;
+    switch (ks) {
+    case 1: qkv_post_kernel<D, 1><<<grid, 64, 0, stream>>>(a); break;
+    case 2: qkv_post_kernel<D, 2><<<grid, 64, 0, stream>>>(a); break;
+    case 3: qkv_post_kernel<D, 3><<<grid, 64, 0, stream>>>(a); break;
+    case 4: qkv_post_kernel<D, 4><<<grid, 64, 0, stream>>>(a); break;
+    default: qkv_post_kernel<D, 0><<<grid, 64, 0, stream>>>(a); break;
+    }
+  };
   switch (a.dimension) {
-  case 128: qkv_post_kernel<128><<<grid, 64, 0, stream>>>(a); break;
-  case 256: qkv_post_kernel<256><<<grid, 64, 0, stream>>>(a); break;
-  case 512: qkv_post_kernel<512><<<grid, 64, 0, stream>>>(a); break;
+  case 128: launch(std::integral_constant<int, 128>{}); break;
+  case 256: launch(std::integral_constant<int, 256>{}); break;
+  case 512: launch(std::integral_constant<int, 512>{}); break;
   default: throw std::runtime_error("QKV post-processing: unsupported head dimension");
   }
   hip_check(hipGetLastError(), "launch QKV post-processing");
