@@ -78,6 +78,8 @@ struct GemmArgs {
 
 // Bytes of the e4m3 activation operand workspace for m rows of k elements.
 size_t gemm_xprep_bytes(int m, int k);
+// 16-token tiles per token block of the e4m3 activation operand for m rows (2 or 8).
+inline int gemm_token_tiles(int m) { return m <= 32 ? 2 : 8; }
 // Keys of the argmax partial workspace for an m-row lm_head of this layout.
 size_t gemm_argmax_partials(int m, const WeightLayout &layout);
 // Split-K factor: a divisor of k_steps (128-byte steps) that fills the GPU.

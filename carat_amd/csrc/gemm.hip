@@ -119,23 +119,25 @@ void launch_pack(const void *src, void *dst, const WeightLayout &l, bool pack, h
 __global__ __launch_bounds__(256) void prepare_x_kernel(const bf16_t *x, int ldx, int m, int k,
                                                         const float *x_amax, int amax_stripes,
                                                         int token_tiles, unsigned char *out) {
-  const float inv = 1.0f / fp8_scale_from_amax(amax_read(x_amax, amax_stripes));
   const int steps = k / kStepBytes;
   const int chunk = blockIdx.x * blockDim.x + threadIdx.x;  // one 16-byte chunk per thread
   const int chunks_per_block = steps * token_tiles * 128;
   const int m_block = blockIdx.y;
-  if (chunk >= chunks_per_block) return;
   const int lane = chunk & 63;
   const int half = (chunk >> 6) & 1;
   const int tile = (chunk >> 7) % token_tiles;
   const int step = (chunk >> 7) / token_tiles;
   const int token = m_block * token_tiles * 16 + tile * 16 + (lane & 15);
   const int group = lane >> 4;
+  // The row slice goes out before the amax: neither load waits for the other. Lanes past the
+  // chunks or tokens re-read a valid slice (token m - 1) and store nothing or zeros.
+  const bf16_t *src = x + static_cast<size_t>(min(token, m - 1)) * ldx + step * 128 + half * 64 + group * 16;
+  const u32x4 lo = *reinterpret_cast<const u32x4 *>(src);
+  const u32x4 hi = *reinterpret_cast<const u32x4 *>(src + 8);
+  const float inv = 1.0f / fp8_scale_from_amax(amax_read(x_amax, amax_stripes));
+  if (chunk >= chunks_per_block) return;
   u32x4 value = {0u, 0u, 0u, 0u};
   if (token < m) {
-    const bf16_t *src = x + static_cast<size_t>(token) * ldx + step * 128 + half * 64 + group * 16;
-    const u32x4 lo = *reinterpret_cast<const u32x4 *>(src);
-    const u32x4 hi = *reinterpret_cast<const u32x4 *>(src + 8);
     const uint32_t w[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
 #pragma unroll
     for (int q = 0; q < 4; ++q)
@@ -540,7 +542,7 @@ void launch_gemm(const GemmArgs &a, hipStream_t stream) {
   const int total_steps = row_bytes / kStepBytes;
   if (total_steps % a.k_splits != 0) throw std::runtime_error("GEMM split-K must divide K steps");
   const bool small_m = a.m <= 32;
-  const int tt = small_m ? 2 : 8;
+  const int tt = gemm_token_tiles(a.m);
   const int tokens_per_block = tt * 16;
   const int m_blocks = (a.m + tokens_per_block - 1) / tokens_per_block;
   check_layout(a.w_layout);
@@ -653,7 +655,7 @@ void unpack_weight(const void *packed, void *row_major, const WeightLayout &layo
 }
 
 size_t gemm_xprep_bytes(int m, int k) {
-  const int tt = m <= 32 ? 2 : 8;
+  const int tt = gemm_token_tiles(m);
   const int m_blocks = (m + tt * 16 - 1) / (tt * 16);
   return static_cast<size_t>(m_blocks) * (k / kStepBytes) * tt * kTileBytes;
 }

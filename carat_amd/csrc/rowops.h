@@ -45,7 +45,18 @@ struct RowArgs {
   bf16_t *y_out = nullptr;
   float *y_amax = nullptr;
   int amax_stripes = 1;            // floats per amax (x_amax and y_amax), see amax_publish
+  // Optional (the verify step's layer-end rows, <= kFusedQuantizeRows rows): y also goes out
+  // quantised to e4m3 with its per-tensor scale (amax / 448), in the fp8 GEMM's activation
+  // operand order (gemm.hip prepare_x_kernel's layout, xprep_token_tiles tiles per token block),
+  // so no separate quantisation kernel runs. The workgroups agree on the amax through `sync`
+  // (two zeroed words, kAmaxStripeFloats floats apart: an arrival counter and the released
+  // amax); a wait that exceeds its bound sets *fault and the output is not to be used.
+  unsigned char *xprep = nullptr;
+  int xprep_token_tiles = 8;
+  unsigned *sync = nullptr;
+  int32_t *fault = nullptr;
 };
+constexpr int kFusedQuantizeRows = 192;  // every row's workgroup is resident at once (256 CUs)
 void launch_row_kernel(const RowArgs &args, hipStream_t stream);
 
 // ---------------------------------------------------------------------------------------------
@@ -85,7 +96,7 @@ struct QkvArgs {
 void launch_qkv_post(const QkvArgs &args, hipStream_t stream);
 
 // Zeroes the stripes of `amax_count` per-step striped amaxes (stripe i at i * kAmaxStripeFloats).
-void launch_step_init(float *amax, int amax_count, hipStream_t stream);
+void launch_step_init(float *amax, int amax_count, hipStream_t stream, int32_t *flag = nullptr);
 
 // ---------------------------------------------------------------------------------------------
 // Acceptance + commit (cuda/batch_model_runner.cu:1735-1808, net effect of ops.cu:827-871).

@@ -13,6 +13,9 @@ constexpr int kRowThreads = 1024;
 constexpr int kQkvUnrolledSplits = 4;  // split-K partials the QKV post-processing loads at once
 constexpr int kMaxAcceptRows = 1024;    // rows per request of a forced (prefill) commit
 constexpr int kRowMaxQuadsPerThread = 4;  // widths up to 16384
+// Polls of the fused quantisation's release word (each an atomic round trip plus a short sleep)
+// before it gives up and reports a fault: far beyond any real wait.
+constexpr int kFusedQuantizeSpins = 1 << 17;
 
 __device__ __forceinline__ float inverse_rms(float square_sum, int width, float eps) {
   return rsqrtf(square_sum / static_cast<float>(width) + eps);
@@ -212,16 +215,86 @@ __global__ __launch_bounds__(kThreads) void layer_end_kernel(const RowArgs a) {
 #pragma unroll
   for (int i = 0; i < Q; ++i) {
     const int q = threadIdx.x + i * kThreads;
-    f32x4_t y;
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      y[c] = round_bf16(v[i][c] * inv * w2[i][c]);
-      amax = fmaxf(amax, fabsf(y[c]));
+      v[i][c] = round_bf16(v[i][c] * inv * w2[i][c]);  // y, kept for the fused quantisation
+      amax = fmaxf(amax, fabsf(v[i][c]));
     }
-    if (q < quads) reinterpret_cast<uint2 *>(a.y_out + row_offset)[q] = f32x4_to_bf16(y);
+    if (q < quads) reinterpret_cast<uint2 *>(a.y_out + row_offset)[q] = f32x4_to_bf16(v[i]);
   }
   amax = block_max(amax, scratch);
-  if (threadIdx.x == 0) amax_publish(a.y_amax, a.amax_stripes, amax);
+  if (a.xprep == nullptr) {
+    if (threadIdx.x == 0) amax_publish(a.y_amax, a.amax_stripes, amax);
+    return;
+  }
+
+  // ---- fused e4m3 quantisation of y. Every workgroup publishes its amax (a returning atomic,
+  // complete before the arrival), then arrives; the last to arrive reads every stripe and
+  // releases the tensor's amax; the others wait for the release. Agent-scope read-modify-writes
+  // are coherent across the XCDs without cache maintenance, so no fence is needed: the only
+  // values exchanged are these atomics.
+  __shared__ float tensor_amax;
+  if (threadIdx.x < kWave) {
+    const int lane = threadIdx.x;
+    unsigned *release = a.sync + kAmaxStripeFloats;
+    int last = 0;
+    if (lane == 0) {
+      unsigned *stripe = reinterpret_cast<unsigned *>(a.y_amax) +
+                         (blockIdx.x % a.amax_stripes) * kAmaxStripeFloats;
+      const unsigned before = __hip_atomic_fetch_max(stripe, __float_as_uint(amax), __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT);
+      __asm__ volatile("s_waitcnt vmcnt(0)" ::"v"(before) : "memory");
+      const unsigned arrived =
+          __hip_atomic_fetch_add(a.sync, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      last = arrived + 1 == gridDim.x;
+    }
+    last = __shfl(last, 0, kWave);
+    float total;
+    if (last) {
+      const unsigned bits = lane < a.amax_stripes
+                                ? __hip_atomic_fetch_max(reinterpret_cast<unsigned *>(a.y_amax) +
+                                                             lane * kAmaxStripeFloats,
+                                                         0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                : 0u;
+      total = wave_max(__uint_as_float(bits));
+      if (lane == 0)
+        (void)__hip_atomic_exchange(release, __float_as_uint(total) | 0x80000000u,
+                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+      unsigned seen = 0;
+      if (lane == 0) {
+        for (int spin = 0; spin < kFusedQuantizeSpins; ++spin) {
+          seen = __hip_atomic_fetch_or(release, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          if (seen & 0x80000000u) break;
+          __builtin_amdgcn_s_sleep(2);
+        }
+        if (!(seen & 0x80000000u))
+          (void)__hip_atomic_fetch_or(a.fault, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      total = __uint_as_float(__shfl(static_cast<int>(seen & 0x7fffffffu), 0, kWave));
+    }
+    if (lane == 0) tensor_amax = total;
+  }
+  __syncthreads();
+  const float q_inv = 1.0f / fp8_scale_from_amax(tensor_amax);
+  // operand layout: [m_block][step][tile][half][lane = group * 16 + col][16 B] with token =
+  // m_block * TT * 16 + tile * 16 + col and K bytes [step * 128 + half * 64 + group * 16, +16)
+  const int tt = a.xprep_token_tiles;
+  const int steps = a.width / 128;
+  const int m_block = row / (tt * 16);
+  const int tile = (row / 16) % tt;
+  const int col = row % 16;
+  unsigned char *block = a.xprep + static_cast<size_t>(m_block) * steps * tt * 128 * 16;
+#pragma unroll
+  for (int i = 0; i < Q; ++i) {
+    const int q = threadIdx.x + i * kThreads;
+    if (q >= quads) continue;
+    const int k = q * 4;
+    const int step = k / 128, half = (k / 64) % 2, group = (k / 16) % 4;
+    const size_t chunk = ((static_cast<size_t>(step) * tt + tile) * 2 + half) * 64 + group * 16 + col;
+    *reinterpret_cast<uint32_t *>(block + chunk * 16 + (k % 16)) =
+        f32x4_to_e4m3x4(v[i][0] * q_inv, v[i][1] * q_inv, v[i][2] * q_inv, v[i][3] * q_inv);
+  }
 }
 
 // One wave per (row, head). Lane l owns elements [l*E, l*E+E) with E = D/64; the rotate-half
@@ -376,9 +449,10 @@ __global__ __launch_bounds__(64) void qkv_post_kernel(const QkvArgs a) {
 }
 
 // Clears every stripe of `amax_count` striped amaxes (stripe i at i * kAmaxStripeFloats).
-__global__ void step_init_kernel(float *amax, int amax_count) {
+__global__ void step_init_kernel(float *amax, int amax_count, int32_t *flag) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i < amax_count) amax[static_cast<size_t>(i) * kAmaxStripeFloats] = 0.0f;
+  if (flag != nullptr && i == 0) *flag = 0;
 }
 
 // Greedy longest-prefix acceptance (cuda/batch_model_runner.cu:1738-1759).
@@ -574,13 +648,32 @@ bool launch_layer_end(const RowArgs &a, hipStream_t stream) {
   const bool fixed = a.source == RowSource::partials && a.x_amax != nullptr &&
                      a.w_scale != nullptr && a.w1 != nullptr && a.residual != nullptr &&
                      a.r1_out != nullptr && a.w2 != nullptr && a.y_out != nullptr &&
-                     a.y_amax != nullptr && a.v_out == nullptr && a.rows < 512;
-  if (!fixed || a.width != 5376 || a.splits < 1 || a.splits > 4) return false;
-  switch (a.splits) {
-  case 1: layer_end_kernel<3, 448, 1><<<a.rows, 448, 0, stream>>>(a); break;
-  case 2: layer_end_kernel<3, 448, 2><<<a.rows, 448, 0, stream>>>(a); break;
-  case 3: layer_end_kernel<3, 448, 3><<<a.rows, 448, 0, stream>>>(a); break;
-  default: layer_end_kernel<3, 448, 4><<<a.rows, 448, 0, stream>>>(a); break;
+                     a.y_amax != nullptr && a.v_out == nullptr && a.rows < 512 &&
+                     a.splits >= 1 && a.splits <= 4;
+  const int quads = a.width / 4;
+  // (quads per thread, threads): 5376 wide rows take 448 x 3 with no idle lane
+  const int q = a.width == 5376 ? 3 : quads <= 1024 ? 1 : quads <= 2048 ? 2 : quads <= 4096 ? 4 : 0;
+  if (a.xprep != nullptr &&
+      (!fixed || q == 0 || a.rows > kFusedQuantizeRows || a.sync == nullptr || a.fault == nullptr ||
+       a.width % 128 != 0 || (a.xprep_token_tiles != 2 && a.xprep_token_tiles != 8)))
+    throw std::runtime_error("fused row quantisation needs the layer-end shape, <= 192 rows and its sync words");
+  if (!fixed || q == 0) return false;
+  auto go = [&](auto quads_per_thread, auto threads) {
+    constexpr int Q = decltype(quads_per_thread)::value;
+    constexpr int T = decltype(threads)::value;
+    switch (a.splits) {
+    case 1: layer_end_kernel<Q, T, 1><<<a.rows, T, 0, stream>>>(a); break;
+    case 2: layer_end_kernel<Q, T, 2><<<a.rows, T, 0, stream>>>(a); break;
+    case 3: layer_end_kernel<Q, T, 3><<<a.rows, T, 0, stream>>>(a); break;
+    default: layer_end_kernel<Q, T, 4><<<a.rows, T, 0, stream>>>(a); break;
+    }
+  };
+  using I = std::integral_constant<int, 1>;
+  switch (q) {
+  case 3: go(std::integral_constant<int, 3>{}, std::integral_constant<int, 448>{}); break;
+  case 1: go(I{}, std::integral_constant<int, 1024>{}); break;
+  case 2: go(std::integral_constant<int, 2>{}, std::integral_constant<int, 1024>{}); break;
+  default: go(std::integral_constant<int, 4>{}, std::integral_constant<int, 1024>{}); break;
   }
   return true;
 }
@@ -657,9 +750,9 @@ void launch_qkv_post(const QkvArgs &a, hipStream_t stream) {
   hip_check(hipGetLastError(), "launch QKV post-processing");
 }
 
-void launch_step_init(float *amax, int amax_count, hipStream_t stream) {
+void launch_step_init(float *amax, int amax_count, hipStream_t stream, int32_t *flag) {
   if (amax_count <= 0) return;
-  step_init_kernel<<<(amax_count + 255) / 256, 256, 0, stream>>>(amax, amax_count);
+  step_init_kernel<<<(amax_count + 255) / 256, 256, 0, stream>>>(amax, amax_count, flag);
   hip_check(hipGetLastError(), "launch step init");
 }
 

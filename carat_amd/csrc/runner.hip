@@ -203,8 +203,12 @@ struct BatchModelRunner::Implementation {
   // device inputs / outputs and their pinned host staging
   DeviceBuffer device_io;
   int32_t *d_tokens = nullptr, *d_positions = nullptr, *d_slots = nullptr, *d_first = nullptr,
-          *d_caps = nullptr, *d_accepted = nullptr, *d_next = nullptr, *d_predictions = nullptr;
+          *d_caps = nullptr, *d_accepted = nullptr, *d_next = nullptr, *d_predictions = nullptr,
+          *d_fault = nullptr;
   int32_t *host_io = nullptr;  // pinned mirror of device_io
+  // verify steps quantise the layer-end rows' outputs in the row kernels (RowArgs::xprep)
+  bool fused_quantize_enabled = true;
+  bool last_input_prepared = false;
   size_t io_ints = 0;
   int sliding_layer_count = 0;
   int last_sliding = -1, last_global = -1;
@@ -610,7 +614,9 @@ struct BatchModelRunner::Implementation {
     attention_out.allocate(sizeof(bf16_t) * M * max_qw);
     final_hidden.allocate(sizeof(bf16_t) * M * H);
     partials.allocate(sizeof(float) * partial);
-    amax.allocate(sizeof(float) * (layers.size() * 4 + 8) * kAmaxSlotFloats);
+    // per-tensor amax slots (four per layer, eight more), then two fused-quantisation sync slots
+    // per layer; step_init clears all of them
+    amax.allocate(sizeof(float) * amax_slot_count() * kAmaxSlotFloats);
     {
       size_t xp = std::max(gemm_xprep_bytes(step_rows, spec.hidden),
                            gemm_xprep_bytes(step_rows, spec.intermediate));
@@ -673,7 +679,8 @@ struct BatchModelRunner::Implementation {
                 "upload sliding-layer table");
 
     // I/O block: tokens[M] positions[B] slots[B] first[B] caps[B] accepted[B] next[B] pred[M]
-    io_ints = 2 * M + 6 * static_cast<size_t>(batch_size);
+    // fault[1] (set by a fused quantisation whose wait exceeded its bound)
+    io_ints = 2 * M + 6 * static_cast<size_t>(batch_size) + 1;
     device_io.allocate(sizeof(int32_t) * io_ints);
     hip_check(hipHostMalloc(reinterpret_cast<void **>(&host_io), sizeof(int32_t) * io_ints),
               "allocate pinned staging");
@@ -686,6 +693,7 @@ struct BatchModelRunner::Implementation {
     d_accepted = d_caps + batch_size;
     d_next = d_accepted + batch_size;
     d_predictions = d_next + batch_size;
+    d_fault = d_predictions + M;
   }
 
   // Per-tensor amax slots, kAmaxStripes stripes each (four per layer, then the lm_head input).
@@ -693,6 +701,12 @@ struct BatchModelRunner::Implementation {
     return amax.as<float>() + (layer * 4 + which) * kAmaxSlotFloats;
   }
   float *lm_head_amax() { return amax.as<float>() + layers.size() * 4 * kAmaxSlotFloats; }
+  size_t amax_slot_count() const { return layers.size() * 6 + 8; }
+  // The two sync slots of layer li's fused layer-end quantisations (0: after O, 1: after down).
+  unsigned *sync_slot(size_t layer, int which) {
+    return reinterpret_cast<unsigned *>(amax.as<float>() +
+                                        (layers.size() * 4 + 8 + layer * 2 + which) * kAmaxSlotFloats);
+  }
 
   void run_fp8_gemm(const bf16_t *x, int rows, int k, const float *x_amax, const PackedWeight &w,
                     const float *w_scale, GemmEpilogue epilogue, bf16_t *y, float *y_amax,
@@ -798,6 +812,10 @@ struct BatchModelRunner::Implementation {
     const int32_t *positions = nullptr, *slots = nullptr;
     bf16_t *input = nullptr, *output = nullptr, *normalized = nullptr;
     float *in_amax = nullptr;
+    // the layer-end rows quantise their output for the next GEMM themselves (verify steps of
+    // <= kFusedQuantizeRows rows; sync slots and the fault flag cleared by this step's step_init)
+    bool fused_quantize = false;
+    bool input_prepared = false;  // the xprep workspace already holds `normalized`, quantised
   };
 
   // Layer li over one step's rows: QKV projection and post-processing (global rows go straight to
@@ -805,8 +823,17 @@ struct BatchModelRunner::Implementation {
   // MLP and the residual; the next layer's normalized input (the final norm after the last layer)
   // goes to next_normalized with its amax in next_amax. The per-layer amax slots 1..3 are this
   // step's (amax_slot).
-  void enqueue_layer(size_t li, const StepIo &io, bf16_t *next_normalized, float *next_amax) {
+  // Returns whether next_normalized also went out quantised into the xprep workspace.
+  bool enqueue_layer(size_t li, const StepIo &io, bf16_t *next_normalized, float *next_amax) {
     const int rows = io.requests * io.depth;
+    const bool fuse = io.fused_quantize && rows <= kFusedQuantizeRows;
+    auto fuse_quantize = [&](RowArgs &r, int which) {
+      if (!fuse) return;
+      r.xprep = xprep.as<unsigned char>();
+      r.xprep_token_tiles = gemm_token_tiles(rows);
+      r.sync = sync_slot(li, which);
+      r.fault = d_fault;
+    };
     TargetLayer &L = layers[li];
     const float *scales = L.scales.as<float>();
     const int D = L.spec.head_dimension;
@@ -814,7 +841,7 @@ struct BatchModelRunner::Implementation {
     int splits = 1;
     run_fp8_gemm(io.normalized, rows, spec.hidden, io.in_amax, L.qkv,
                  scales + 0, GemmEpilogue::partial_f32, nullptr, nullptr,
-                 &splits, probe_qkv_gemm);
+                 &splits, probe_qkv_gemm, io.input_prepared);
     QkvArgs q;
     q.amax_stripes = kAmaxStripes;
     q.partials = partials.as<float>();
@@ -891,11 +918,12 @@ struct BatchModelRunner::Implementation {
     ro.w2 = L.pre_mlp_norm.as<bf16_t>();
     ro.y_out = pre_mlp.as<bf16_t>();
     ro.y_amax = amax_slot(li, 2);
+    fuse_quantize(ro, 0);
     launch_row_kernel(ro, stream);
     // gate/up with the GELU gate fused
     run_fp8_gemm(pre_mlp.as<bf16_t>(), rows, spec.hidden, amax_slot(li, 2), L.gate_up,
                  scales + 2, GemmEpilogue::gelu_gate,
-                 activated.as<bf16_t>(), amax_slot(li, 3), nullptr, probe_gate_up_gemm);
+                 activated.as<bf16_t>(), amax_slot(li, 3), nullptr, probe_gate_up_gemm, fuse);
     // down + post-MLP norm + residual + layer scalar + next input norm
     run_fp8_gemm(activated.as<bf16_t>(), rows, spec.intermediate, amax_slot(li, 3),
                  L.down, scales + 3, GemmEpilogue::partial_f32, nullptr,
@@ -918,7 +946,9 @@ struct BatchModelRunner::Implementation {
                                     : layers[li + 1].input_norm.as<bf16_t>();
     rd.y_out = next_normalized;
     rd.y_amax = next_amax;
+    fuse_quantize(rd, 1);
     launch_row_kernel(rd, stream);
+    return fuse;
   }
 
   void enqueue_embedding(const int32_t *tokens, int rows, bf16_t *hidden, bf16_t *normalized_out,
@@ -972,8 +1002,8 @@ struct BatchModelRunner::Implementation {
                       bool lm_head_pass = true) {
     const int rows = requests * depth;
     last_rows = rows;
-    launch_step_init(amax.as<float>(), static_cast<int>((layers.size() * 4 + 8) * kAmaxStripes),
-                     stream);
+    launch_step_init(amax.as<float>(), static_cast<int>(amax_slot_count() * kAmaxStripes), stream,
+                     d_fault);
     enqueue_embedding(d_tokens, rows, hidden_a.as<bf16_t>(), normalized.as<bf16_t>(),
                       amax_slot(0, 0));
     StepIo io;
@@ -984,11 +1014,14 @@ struct BatchModelRunner::Implementation {
     io.input = hidden_a.as<bf16_t>();
     io.output = hidden_b.as<bf16_t>();
     io.normalized = normalized.as<bf16_t>();
+    io.fused_quantize = fused_quantize_enabled;
     for (size_t li = 0; li < layers.size(); ++li) {
       io.in_amax = amax_slot(li, 0);
       const bool last = li + 1 == layers.size();
-      enqueue_layer(li, io, last ? final_hidden.as<bf16_t>() : normalized.as<bf16_t>(),
-                    last ? lm_head_amax() : amax_slot(li + 1, 0));
+      io.input_prepared = enqueue_layer(li, io, last ? final_hidden.as<bf16_t>() : normalized.as<bf16_t>(),
+                                        last ? lm_head_amax() : amax_slot(li + 1, 0)) &&
+                          !last;
+      if (last) last_input_prepared = io.fused_quantize && rows <= kFusedQuantizeRows;
       std::swap(io.input, io.output);
     }
     // lm_head + argmax (a forced prefill step whose predictions nobody reads skips it; the
@@ -996,7 +1029,8 @@ struct BatchModelRunner::Implementation {
     if (lm_head_pass)
       run_fp8_gemm(final_hidden.as<bf16_t>(), rows, spec.hidden, lm_head_amax(),
                    lm_head, embedding_scale.as<float>(),
-                   GemmEpilogue::argmax, nullptr, nullptr, nullptr, probe_lm_head_gemm);
+                   GemmEpilogue::argmax, nullptr, nullptr, nullptr, probe_lm_head_gemm,
+                   last_input_prepared);
     enqueue_accept(requests, depth, has_caps, force_accept, d_positions, d_slots, 0,
                    sliding_layer_count, final_hidden.as<bf16_t>(), !lm_head_pass);
   }
@@ -1250,7 +1284,7 @@ struct BatchModelRunner::Implementation {
       const PrefillStep &step = state.steps[s];
       const int requests = static_cast<int>(step.requests.size());
       const size_t row0 = state.step_row0[s];
-      launch_step_init(amax.as<float>(), static_cast<int>((layers.size() * 4 + 8) * kAmaxStripes),
+      launch_step_init(amax.as<float>(), static_cast<int>(amax_slot_count() * kAmaxStripes),
                        stream);
       StepIo io;
       io.requests = requests;
@@ -1426,10 +1460,13 @@ struct BatchModelRunner::Implementation {
     hip_check(hipEventRecord(stop_event, stream), "record verify stop");
     int32_t *h_accepted = h_caps + batch_size;
     hip_check(hipMemcpyAsync(h_accepted, d_accepted,
-                             sizeof(int32_t) * (2 * static_cast<size_t>(batch_size) + M),
+                             sizeof(int32_t) * (2 * static_cast<size_t>(batch_size) + M + 1),
                              hipMemcpyDeviceToHost, stream),
               "copy speculative results");
     hip_check(hipStreamSynchronize(stream), "synchronize speculative verification");
+    if (h_accepted[2 * static_cast<size_t>(batch_size) + M] != 0)
+      throw std::runtime_error(
+          "fused activation quantisation timed out waiting for the step's workgroups");
     hip_check(hipEventElapsedTime(&verify_ms, start_event, stop_event), "verify timing");
     collect_probes();
     int32_t *h_next = h_accepted + batch_size;
