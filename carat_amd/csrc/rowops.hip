@@ -154,14 +154,14 @@ __global__ __launch_bounds__(kThreads) void row_kernel(const RowArgs a) {
 // 448 threads x 3 quads, no idle lanes). Every global load of the row is issued in one straight
 // run before the first reduction (no conditional load: the layer scalar's address is selected,
 // not branched on); the runtime options of row_kernel put waits between them.
-template <int Q, int kThreads, int kSplits>
+template <int Q, int kThreads, int kSplits, bool kScaled = true>
 __global__ __launch_bounds__(kThreads) void layer_end_kernel(const RowArgs a) {
   constexpr int kWaves = kThreads / kWave;
   __shared__ float scratch[kWaves];
   const int row = blockIdx.x;
   const int quads = a.width / 4;
   const size_t row_offset = static_cast<size_t>(row) * a.width;
-  const float w_scale = *a.w_scale;
+  const float w_scale = kScaled ? *a.w_scale : 1.0f;
   const float layer_scalar = bf16_to_f32(*(a.scalar != nullptr ? a.scalar : a.w2));
   f32x4_t v[Q], w1[Q], res[Q], w2[Q];
   f32x4_t part[Q][kSplits];
@@ -175,8 +175,8 @@ __global__ __launch_bounds__(kThreads) void layer_end_kernel(const RowArgs a) {
     res[i] = bf16x4_to_f32(reinterpret_cast<const uint2 *>(a.residual + row_offset)[q]);
     w2[i] = bf16x4_to_f32(reinterpret_cast<const uint2 *>(a.w2)[q]);
   }
-  const float amax_part = amax_lane(a.x_amax, a.amax_stripes);
-  const float scale = w_scale * fp8_scale_from_amax(wave_max(amax_part));
+  float scale = 1.0f;
+  if constexpr (kScaled) scale = w_scale * fp8_scale_from_amax(wave_max(amax_lane(a.x_amax, a.amax_stripes)));
 
   float square_sum = 0.0f;
 #pragma unroll
@@ -222,6 +222,7 @@ __global__ __launch_bounds__(kThreads) void layer_end_kernel(const RowArgs a) {
     }
     if (q < quads) reinterpret_cast<uint2 *>(a.y_out + row_offset)[q] = f32x4_to_bf16(v[i]);
   }
+  if (a.y_amax == nullptr) return;  // bf16 consumers (the assistant's GEMMs) need no amax
   amax = block_max(amax, scratch);
   if (a.xprep == nullptr) {
     if (threadIdx.x == 0) amax_publish(a.y_amax, a.amax_stripes, amax);
@@ -645,32 +646,39 @@ __global__ __launch_bounds__(256) void argmax_accept_final_kernel(const ArgmaxAc
 namespace {
 // The layer-end shape of the verify step (see layer_end_kernel); false when it does not apply.
 bool launch_layer_end(const RowArgs &a, hipStream_t stream) {
-  const bool fixed = a.source == RowSource::partials && a.x_amax != nullptr &&
-                     a.w_scale != nullptr && a.w1 != nullptr && a.residual != nullptr &&
-                     a.r1_out != nullptr && a.w2 != nullptr && a.y_out != nullptr &&
-                     a.y_amax != nullptr && a.v_out == nullptr && a.rows < 512 &&
-                     a.splits >= 1 && a.splits <= 4;
+  // fp8 projections' partials carry their scale operands; bf16 ones (the assistant) none
+  const bool scaled = a.x_amax != nullptr && a.w_scale != nullptr;
+  const bool fixed = a.source == RowSource::partials && (scaled || (a.x_amax == nullptr && a.w_scale == nullptr)) &&
+                     a.w1 != nullptr && a.residual != nullptr && a.r1_out != nullptr &&
+                     a.w2 != nullptr && a.y_out != nullptr && (a.y_amax != nullptr || !scaled) &&
+                     a.v_out == nullptr && a.rows < 512 && a.splits >= 1 && a.splits <= 4;
   const int quads = a.width / 4;
   // (quads per thread, threads): 5376 wide rows take 448 x 3 with no idle lane
-  const int q = a.width == 5376 ? 3 : quads <= 1024 ? 1 : quads <= 2048 ? 2 : quads <= 4096 ? 4 : 0;
+  const int q = a.width == 5376 ? 3 : quads <= 256 ? 5 : quads <= 1024 ? 1 : quads <= 2048 ? 2 : quads <= 4096 ? 4 : 0;
   if (a.xprep != nullptr &&
-      (!fixed || q == 0 || a.rows > kFusedQuantizeRows || a.sync == nullptr || a.fault == nullptr ||
-       a.width % 128 != 0 || (a.xprep_token_tiles != 2 && a.xprep_token_tiles != 8)))
+      (!fixed || !scaled || q == 0 || a.rows > kFusedQuantizeRows || a.sync == nullptr ||
+       a.fault == nullptr || a.y_amax == nullptr || a.width % 128 != 0 ||
+       (a.xprep_token_tiles != 2 && a.xprep_token_tiles != 8)))
     throw std::runtime_error("fused row quantisation needs the layer-end shape, <= 192 rows and its sync words");
   if (!fixed || q == 0) return false;
   auto go = [&](auto quads_per_thread, auto threads) {
     constexpr int Q = decltype(quads_per_thread)::value;
     constexpr int T = decltype(threads)::value;
-    switch (a.splits) {
-    case 1: layer_end_kernel<Q, T, 1><<<a.rows, T, 0, stream>>>(a); break;
-    case 2: layer_end_kernel<Q, T, 2><<<a.rows, T, 0, stream>>>(a); break;
-    case 3: layer_end_kernel<Q, T, 3><<<a.rows, T, 0, stream>>>(a); break;
-    default: layer_end_kernel<Q, T, 4><<<a.rows, T, 0, stream>>>(a); break;
-    }
+    auto pick = [&](auto scaled_constant) {
+      constexpr bool S = decltype(scaled_constant)::value;
+      switch (a.splits) {
+      case 1: layer_end_kernel<Q, T, 1, S><<<a.rows, T, 0, stream>>>(a); break;
+      case 2: layer_end_kernel<Q, T, 2, S><<<a.rows, T, 0, stream>>>(a); break;
+      case 3: layer_end_kernel<Q, T, 3, S><<<a.rows, T, 0, stream>>>(a); break;
+      default: layer_end_kernel<Q, T, 4, S><<<a.rows, T, 0, stream>>>(a); break;
+      }
+    };
+    if (scaled) pick(std::true_type{}); else pick(std::false_type{});
   };
   using I = std::integral_constant<int, 1>;
   switch (q) {
   case 3: go(std::integral_constant<int, 3>{}, std::integral_constant<int, 448>{}); break;
+  case 5: go(I{}, std::integral_constant<int, 256>{}); break;  // rows up to 1024 wide
   case 1: go(I{}, std::integral_constant<int, 1024>{}); break;
   case 2: go(std::integral_constant<int, 2>{}, std::integral_constant<int, 1024>{}); break;
   default: go(std::integral_constant<int, 4>{}, std::integral_constant<int, 1024>{}); break;
