@@ -125,6 +125,45 @@ def gate_up_bytes(hidden, intermediate, rows):
     return 2 * intermediate * hidden + rows * hidden + rows * intermediate * 2
 
 
+def gemm_plan(n, k, gate_up):
+    import ctypes
+    from carat_amd import _lib
+    f, w, sp = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    _lib.check(_lib.lib().carat_hip_gemm_plan(n, k, 1, int(gate_up), ctypes.byref(f), ctypes.byref(w),
+                                              ctypes.byref(sp)))
+    return f.value, w.value, sp.value
+
+
+def gemm_table(runner, desc, rows):
+    """Every per-layer fp8 GEMM of the verify step timed back to back over all 60 layers' weights
+    (stream_gemm_probe, two passes): HBM fraction of 8 TB/s over the algorithmic bytes (e4m3
+    weights + e4m3 activations + outputs: fp32 split-K partials or the bf16 GELU output), raw fp8
+    MFMA use (2*M*N*K flops per launch / 5 PFLOP/s), and the attainable MFMA use at that
+    arithmetic intensity (min(1, AI * 8 TB/s / 5 PFLOP/s))."""
+    H, I = desc.hidden, desc.intermediate
+    g = next(l for l in desc.layers if not l.sliding)
+    qkv_n = (g.query_heads + 2 * g.kv_heads) * g.head_dimension
+    shapes = {"qkv_gemm": (qkv_n, H, False), "o_gemm": (H, g.query_heads * g.head_dimension, False),
+              "gate_up_gemm": (2 * I, H, True), "down_gemm": (H, I, False)}
+    out = {}
+    for kind, (n, k, gate_up) in shapes.items():
+        f, w, splits = gemm_plan(n, k, gate_up)
+        avg_ms, launches = runner.stream_gemm_probe(kind, passes=2)
+        out_bytes = rows * (n // 2) * 2 if gate_up else splits * rows * n * 4
+        nbytes = n * k + rows * k + out_bytes
+        flops = 2.0 * rows * n * k
+        us = avg_ms * 1e3
+        gbs = nbytes / us / 1e3
+        util = flops / (us * 1e-6) / (FP8_PEAK_TFLOPS * 1e12)
+        attainable = min(1.0, flops / nbytes * HBM_PEAK_GBS * 1e9 / (FP8_PEAK_TFLOPS * 1e12))
+        out[kind.replace("_gemm", "")] = {
+            "n": n, "k": k, "layout": f"F{f}/W{w}", "splits": splits, "avg_launch_us": round(us, 2),
+            "bytes_per_launch": nbytes, "GB_s": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+            "mfma_util": round(util, 4), "mfma_attainable": round(attainable, 4),
+            "frac_of_attainable": round(util / attainable, 4)}
+    return out
+
+
 def cpu_baseline(mean_accepted_per_step):
     """Plain OpenMP C evaluation (the oracle, a restatement of the reference's verify layer) timed
     on this host over a bounded sample: one sliding and one global layer at the full config-5 shape,
@@ -470,6 +509,7 @@ def main() -> int:
             f"wall={1e3 * (s1 - s0):.2f}ms draft={runner.timing()[1]:.2f}ms "
             f"verify={runner.timing()[0]:.2f}ms{' (timed)' if timed else ''}")
     avg_launch_ms, probe_launches = runner.stream_gemm_probe("gate_up_gemm", passes=2)
+    gemms = gemm_table(runner, desc, SLOTS * DEPTH)
     # the global verify attention, timed with HIP events around each launch of one dry verify
     runner.set_probe("global_attention")
     runner.read_probe()
@@ -477,6 +517,13 @@ def main() -> int:
     attn_positions = [runner.slot_position(s) for s in slots]
     runner.verify_greedy_proposals(props.tolist(), forced.tolist(), slots, [0] * SLOTS)
     attn_ms, attn_launches = runner.read_probe()
+    # the sliding verify attention the same way (50 launches per verify)
+    runner.set_probe("sliding_attention")
+    runner.read_probe()
+    props = planted_proposals(runner, forced, slots, rng, desc.vocabulary)
+    sliding_positions = [runner.slot_position(s) for s in slots]
+    runner.verify_greedy_proposals(props.tolist(), forced.tolist(), slots, [0] * SLOTS)
+    sliding_ms, sliding_launches = runner.read_probe()
     runner.set_probe(None)
 
     breakdown = {}
@@ -541,14 +588,14 @@ def main() -> int:
         },
     }
     g = next(l for l in desc.layers if not l.sliding)
-    attn_bytes = global_attention_bytes(attn_positions, DEPTH + 1, g.kv_heads, g.head_dimension,
+    attn_bytes = global_attention_bytes(attn_positions, DEPTH, g.kv_heads, g.head_dimension,
                                         g.query_heads)
     attn_us = 1e3 * attn_ms / max(attn_launches, 1)
     attn_achieved = attn_bytes / (attn_us * 1e-6) / 1e9
     # the other kernel family of the same weight: global verify attention (10 launches per step)
     result["roofline_attention"] = {
         "kernel": f"global verify attention (24 slots x {g.kv_heads} kv heads, D {g.head_dimension}, "
-                  f"~{attn_positions[0] + DEPTH + 1} keys)",
+                  f"~{attn_positions[0] + DEPTH} keys)",
         "bound": "hbm",
         "achieved": round(attn_achieved, 1),
         "peak": HBM_PEAK_GBS,
@@ -558,6 +605,26 @@ def main() -> int:
         "avg_launch_us": round(attn_us, 2),
         "launches": attn_launches,
         "bytes_per_launch": attn_bytes,
+    }
+    result["gemms"] = gemms
+    sl = next(l for l in desc.layers if l.sliding)
+    window = desc.sliding_window
+    sliding_keys = sum(min(int(p), window - 1) + DEPTH for p in sliding_positions)
+    sliding_bytes = (sliding_keys * sl.kv_heads * sl.head_dimension * 2 * 2 +
+                     2 * SLOTS * DEPTH * sl.query_heads * sl.head_dimension * 2)
+    sliding_us = 1e3 * sliding_ms / max(sliding_launches, 1)
+    result["roofline_attention_sliding"] = {
+        "kernel": f"sliding verify attention (24 slots x {sl.kv_heads} kv heads, D {sl.head_dimension}, "
+                  f"{window}-key window + {DEPTH} rows)",
+        "bound": "hbm",
+        "achieved": round(sliding_bytes / (sliding_us * 1e-6) / 1e9, 1),
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": round(sliding_bytes / (sliding_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+        "avg_launch_us": round(sliding_us, 2),
+        "launches": sliding_launches,
+        "bytes_per_launch": sliding_bytes,
+        "timing": "HIP events around each launch of one dry verify (includes the event overhead)",
     }
     if breakdown:
         result["kernels_ms_per_verify"] = breakdown
