@@ -6,8 +6,8 @@ hidden 5376, intermediate 21504, 32 query / 16 KV heads x 128, vocab 262144) and
 4-layer assistant (hidden 1024 on the 5376 backbone, the reference's assistant dims), 24 slots with
 ~8.1k-token contexts, prefilled (untimed) from seeded random token ids through the runner's own
 prefill_slots_chunks. One step = the reference scheduler's speculative cycle
-(native_runtime_main.cpp:583-678): draft_four (forced + 4 drafts) -> acceptance caps ->
-verify_greedy_proposals -> commit_speculation. Drafts are overwritten, before verification, with
+(native_runtime_main.cpp:583-678, run in C++ by carat_hip_bench_speculative_cycle): draft_four
+(forced + 4 drafts) -> acceptance caps -> verify_greedy_proposals -> commit_speculation. Drafts are overwritten, before verification, with
 the target's own greedy chain (computed untimed by dry verifies that commit nothing) so that each
 draft matches with probability 0.7 (geometric acceptance), as config 5 specifies.
 
@@ -448,7 +448,7 @@ def main() -> int:
         print(json.dumps(prefill_throughput(args.prefill, args.seed)))
         return 0
     from carat_amd import lib
-    from carat_amd.runner import BatchModelRunner, ModelDesc, acceptance_cap, commit_speculation
+    from carat_amd.runner import BatchModelRunner, ModelDesc
 
     if args.calibrate_copy:
         import torch
@@ -486,27 +486,18 @@ def main() -> int:
     for step in range(total):
         proposals = planted_proposals(runner, forced, slots, rng, desc.vocabulary)
         timed = step >= args.warmup
-        lib().carat_hip_synchronize()
-        s0 = time.perf_counter()
-        drafts = runner.draft_four(last.tolist(), slots, forced.tolist(), DEPTH)
-        caps = [acceptance_cap(DEPTH, remaining, drafts[r], []) for r in range(SLOTS)]
-        res = runner.verify_greedy_proposals(proposals.tolist(), forced.tolist(), slots, caps)
-        for r in range(SLOTS):
-            a = res.accepted_tokens[r]
-            resident, _, nxt, _ = commit_speculation(int(forced[r]), proposals[r, 1:a].tolist(),
-                                                     res.next_tokens[r], [])
-            last[r] = resident[-1]
-            forced[r] = nxt
-        lib().carat_hip_synchronize()
-        s1 = time.perf_counter()
+        # one scheduler cycle in C++ (draft_four -> acceptance_cap -> verify_greedy_proposals ->
+        # commit_speculation), timed on the host clock from a synchronised device
+        acc, forced, last, seconds = runner.bench_speculative_cycle(last, slots, forced, proposals,
+                                                                    remaining)
         if timed:
-            timed_s += s1 - s0
-            accepted_total += sum(res.accepted_tokens)
+            timed_s += seconds
+            accepted_total += int(acc.sum())
             v_ms, d_ms = runner.timing()
             verify_ms += v_ms
             draft_ms += d_ms
-        log(f"step {step}: accepted={res.accepted_tokens[:8]}... sum={sum(res.accepted_tokens)} "
-            f"wall={1e3 * (s1 - s0):.2f}ms draft={runner.timing()[1]:.2f}ms "
+        log(f"step {step}: accepted={acc[:8].tolist()}... sum={int(acc.sum())} "
+            f"wall={1e3 * seconds:.2f}ms draft={runner.timing()[1]:.2f}ms "
             f"verify={runner.timing()[0]:.2f}ms{' (timed)' if timed else ''}")
     avg_launch_ms, probe_launches = runner.stream_gemm_probe("gate_up_gemm", passes=2)
     gemms = gemm_table(runner, desc, SLOTS * DEPTH)

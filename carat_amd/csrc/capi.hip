@@ -11,7 +11,9 @@
 #include "runner.h"
 #include "speculation.h"
 
+#include <chrono>
 #include <cstring>
+#include <unordered_set>
 #include <map>
 #include <mutex>
 #include <string>
@@ -433,6 +435,50 @@ int carat_hip_runner_verify(carat_hip_runner *runner, int requests, int depth,
     if (accepted_out != nullptr) std::copy(result.accepted_tokens.begin(), result.accepted_tokens.end(), accepted_out);
     if (next_out != nullptr) std::copy(result.next_tokens.begin(), result.next_tokens.end(), next_out);
     if (predictions_out != nullptr) std::copy(r.last_predictions().begin(), r.last_predictions().end(), predictions_out);
+  });
+}
+
+int carat_hip_bench_speculative_cycle(carat_hip_runner *runner, int requests, int depth,
+                                      const int32_t *last_tokens, const int32_t *slots,
+                                      const int32_t *forced, const int32_t *planted,
+                                      int remaining, const int32_t *stop_ids, int stop_count,
+                                      int32_t *accepted_out, int32_t *next_out,
+                                      int32_t *last_out, double *seconds_out) {
+  return guarded([&] {
+    auto &r = runner_of(runner);
+    if (requests <= 0 || depth <= 0 || last_tokens == nullptr || slots == nullptr ||
+        forced == nullptr || planted == nullptr || accepted_out == nullptr ||
+        next_out == nullptr || last_out == nullptr || seconds_out == nullptr ||
+        (stop_count > 0 && stop_ids == nullptr))
+      throw std::runtime_error("invalid speculative cycle arguments");
+    const std::unordered_set<int> stops(stop_ids, stop_ids + std::max(stop_count, 0));
+    const std::vector<int> last(last_tokens, last_tokens + requests);
+    const std::vector<int> slot_list(slots, slots + requests);
+    const std::vector<int> first(forced, forced + requests);
+    std::vector<std::vector<int>> proposals(static_cast<size_t>(requests));
+    for (int i = 0; i < requests; ++i)
+      proposals[static_cast<size_t>(i)].assign(planted + static_cast<size_t>(i) * depth,
+                                               planted + static_cast<size_t>(i + 1) * depth);
+    hip_check(hipDeviceSynchronize(), "synchronise before the speculative cycle");
+    const auto start = std::chrono::steady_clock::now();
+    // native_runtime_main.cpp:583-678: draft, caps from the draft, verify, commit
+    const auto drafts = r.draft_four(last, slot_list, first, depth);
+    std::vector<int> caps(static_cast<size_t>(requests));
+    for (int i = 0; i < requests; ++i)
+      caps[static_cast<size_t>(i)] = acceptance_cap(depth, remaining, drafts[static_cast<size_t>(i)], stops);
+    const GreedyVerificationResult result = r.verify_greedy_proposals(proposals, first, slot_list, caps);
+    for (int i = 0; i < requests; ++i) {
+      const int a = result.accepted_tokens[static_cast<size_t>(i)];
+      const auto &row = proposals[static_cast<size_t>(i)];
+      const std::span<const int> accepted_drafts(row.data() + 1, a > 1 ? static_cast<size_t>(a - 1) : 0);
+      const SpeculativeCommit commit =
+          commit_speculation(first[static_cast<size_t>(i)], accepted_drafts,
+                             result.next_tokens[static_cast<size_t>(i)], stops);
+      accepted_out[i] = a;
+      next_out[i] = commit.next_token;
+      last_out[i] = commit.resident_tokens.back();
+    }
+    *seconds_out = std::chrono::duration<double>(std::chrono::steady_clock::now() - start).count();
   });
 }
 

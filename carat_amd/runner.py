@@ -134,6 +134,22 @@ class BatchModelRunner:
         self.last_predictions = []
         return self
 
+    def bench_speculative_cycle(self, last_tokens, slots, forced, planted, remaining, stop_ids=()):
+        """One scheduler cycle in C++ (carat_hip_bench_speculative_cycle): draft, caps, verify of
+        `planted`, commit. Returns (accepted, next forced tokens, last resident tokens, seconds)."""
+        planted = np.ascontiguousarray(planted, dtype=np.int32)
+        requests, depth = planted.shape
+        stops = _i32(stop_ids)
+        acc = np.zeros(requests, np.int32)
+        nxt = np.zeros(requests, np.int32)
+        last = np.zeros(requests, np.int32)
+        seconds = ctypes.c_double()
+        check(lib().carat_hip_bench_speculative_cycle(
+            self._handle, requests, depth, ptr(_i32(last_tokens)), ptr(_i32(slots)), ptr(_i32(forced)),
+            ptr(planted), remaining, ptr(stops) if stops.size else None, int(stops.size), ptr(acc),
+            ptr(nxt), ptr(last), ctypes.byref(seconds)))
+        return acc, nxt, last, seconds.value
+
     SEGMENT_FN = ctypes.CFUNCTYPE(ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
                                   ctypes.c_char_p, ctypes.POINTER(ctypes.c_void_p))
 

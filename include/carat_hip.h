@@ -200,6 +200,18 @@ int carat_hip_runner_copy_tensor(carat_hip_runner *runner, const char *name, voi
                                  size_t bytes, int direction);
 int carat_hip_runner_set_graphs(carat_hip_runner *runner, int enabled);
 int carat_hip_runner_timing(carat_hip_runner *runner, float *verify_ms, float *draft_ms);
+/* Benchmark helper, no counterpart in the reference: one speculative cycle of the reference's
+ * scheduler (native_runtime_main.cpp:583-678) in C++ -- draft_four(last, slots, forced, depth),
+ * acceptance_cap per request over the drafts, verify_greedy_proposals over `planted` [requests]
+ * [depth] (the benchmark's proposals, row 0 = forced) with those caps, commit_speculation per
+ * request -- timed on the host clock from a synchronised device (*seconds_out). Writes the
+ * accepted counts, the next forced token and the last resident token of every request. */
+int carat_hip_bench_speculative_cycle(carat_hip_runner *runner, int requests, int depth,
+                                      const int32_t *last_tokens, const int32_t *slots,
+                                      const int32_t *forced, const int32_t *planted,
+                                      int remaining, const int32_t *stop_ids, int stop_count,
+                                      int32_t *accepted_out, int32_t *next_out,
+                                      int32_t *last_out, double *seconds_out);
 /* Timing probes: hip events around every launch of one verify-step kernel kind (0 qkv GEMM, 1 O
  * GEMM, 2 gate/up GEMM, 3 down GEMM, 4 lm_head GEMM, 5 sliding attention, 6 global attention;
  * -1 off). Probing runs the verify step without HIP graphs. read_probe returns and resets the sums. */

@@ -113,3 +113,42 @@ def test_speculative_decode_cycles(torch_cuda):
         assert all(len(s.output) > 1 for s in state)
     finally:
         runner.close()
+
+
+def test_bench_cycle_equals_the_python_cycle(torch_cuda):
+    """carat_hip_bench_speculative_cycle (the benchmark's cycle in C++) makes the same decisions as
+    the same cycle composed from the Python mirror: identical accepted counts, next forced tokens,
+    last resident tokens and slot positions on two runners built from the same seed."""
+    desc = tiny_desc()
+    rng = np.random.default_rng(43)
+    say("case: bench cycle (C++) vs python cycle")
+    a = BatchModelRunner(desc, BATCH, MAX_CONTEXT)
+    b = BatchModelRunner(desc, BATCH, MAX_CONTEXT)
+    try:
+        slots = list(range(BATCH))
+        for r in (a, b):
+            r.seed_random_cache(50, seed=3, stddev=1 / math.sqrt(128))
+        forced = rng.integers(0, desc.vocabulary, BATCH).astype(np.int32)
+        last = rng.integers(0, desc.vocabulary, BATCH).astype(np.int32)
+        for cycle in range(3):
+            planted = rng.integers(0, desc.vocabulary, (BATCH, DEPTH + 1)).astype(np.int32)
+            planted[:, 0] = forced
+            acc, nxt, lst, seconds = a.bench_speculative_cycle(last, slots, forced, planted, 3, [7])
+            assert seconds > 0.0
+            drafts = b.draft_four(last.tolist(), slots, forced.tolist(), DEPTH + 1)
+            caps = [acceptance_cap(DEPTH + 1, 3, drafts[i], [7]) for i in range(BATCH)]
+            res = b.verify_greedy_proposals(planted.tolist(), forced.tolist(), slots, caps)
+            want_next, want_last = [], []
+            for i in range(BATCH):
+                k = res.accepted_tokens[i]
+                resident, _, n, _ = commit_speculation(int(forced[i]), planted[i, 1:k].tolist(),
+                                                       res.next_tokens[i], [7])
+                want_next.append(n)
+                want_last.append(resident[-1])
+            assert acc.tolist() == res.accepted_tokens
+            assert nxt.tolist() == want_next and lst.tolist() == want_last
+            assert [a.slot_position(s) for s in slots] == [b.slot_position(s) for s in slots]
+            forced, last = nxt, lst
+    finally:
+        a.close()
+        b.close()
