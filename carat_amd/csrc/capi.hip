@@ -581,6 +581,10 @@ int carat_hip_runner_copy_tensor(carat_hip_runner *runner, const char *name, voi
 int carat_hip_runner_set_graphs(carat_hip_runner *runner, int enabled) {
   return guarded([&] { runner_of(runner).set_graphs_enabled(enabled != 0); });
 }
+
+int carat_hip_runner_set_fused_quantization(carat_hip_runner *runner, int enabled) {
+  return guarded([&] { runner_of(runner).set_fused_quantization(enabled != 0); });
+}
 int carat_hip_runner_set_probe(carat_hip_runner *runner, int kind) {
   return guarded([&] { runner_of(runner).set_probe(kind); });
 }

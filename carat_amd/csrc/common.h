@@ -182,6 +182,57 @@ __device__ __forceinline__ float amax_read(const float *amax, int stripes) {
   return wave_max(amax_lane(amax, stripes));
 }
 
+// Grid-wide agreement on a per-tensor amax among co-resident workgroups (the fused activation
+// quantisations). One wave per workgroup calls it, every lane, with the workgroup's amax: the
+// workgroup publishes its amax on a stripe (a returning atomic, complete before the arrival),
+// then arrives on sync[0]; the last to arrive reads every stripe and releases the tensor's amax
+// (bit 31 set) in sync[kAmaxStripeFloats]; the others poll the release word. Agent-scope
+// read-modify-writes are coherent across the XCDs without cache maintenance, so no fence is
+// needed: the only values exchanged are these atomics. `sync` must be zeroed beforehand;
+// `workgroups` is the number that arrive. A wait past kFusedQuantizeSpins polls sets *fault (the
+// result is then not to be used) and returns. The arriving workgroups must be resident at once,
+// or the early ones wait for the bound.
+constexpr int kFusedQuantizeSpins = 1 << 17;
+__device__ __forceinline__ float fused_amax_release(float *amax, int stripes, unsigned *sync,
+                                                    int32_t *fault, unsigned workgroups,
+                                                    float workgroup_amax) {
+  const int lane = threadIdx.x & (kWave - 1);
+  unsigned *release = sync + kAmaxStripeFloats;
+  const unsigned flat = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+  int last = 0;
+  if (lane == 0) {
+    unsigned *stripe = reinterpret_cast<unsigned *>(amax) + (flat % stripes) * kAmaxStripeFloats;
+    const unsigned before = __hip_atomic_fetch_max(stripe, __float_as_uint(workgroup_amax),
+                                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::"v"(before) : "memory");
+    const unsigned arrived = __hip_atomic_fetch_add(sync, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last = arrived + 1 == workgroups;
+  }
+  last = __shfl(last, 0, kWave);
+  if (last) {
+    const unsigned bits =
+        lane < stripes ? __hip_atomic_fetch_max(reinterpret_cast<unsigned *>(amax) + lane * kAmaxStripeFloats,
+                                                0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                       : 0u;
+    const float total = wave_max(__uint_as_float(bits));
+    if (lane == 0)
+      (void)__hip_atomic_exchange(release, __float_as_uint(total) | 0x80000000u, __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT);
+    return total;
+  }
+  unsigned seen = 0;
+  if (lane == 0) {
+    for (int spin = 0; spin < kFusedQuantizeSpins; ++spin) {
+      seen = __hip_atomic_fetch_or(release, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (seen & 0x80000000u) break;
+      __builtin_amdgcn_s_sleep(2);
+    }
+    if (!(seen & 0x80000000u))
+      (void)__hip_atomic_fetch_or(fault, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  return __uint_as_float(__shfl(static_cast<int>(seen & 0x7fffffffu), 0, kWave));
+}
+
 // ---------------------------------------------------------------------------------------------
 // argmax keys: an order-preserving 64-bit key (value bits << 32 | ~index) so that an unsigned
 // max picks the largest value and, among equal values, the LOWEST index -- the tie rule of the

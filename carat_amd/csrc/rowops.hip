@@ -13,9 +13,6 @@ constexpr int kRowThreads = 1024;
 constexpr int kQkvUnrolledSplits = 4;  // split-K partials the QKV post-processing loads at once
 constexpr int kMaxAcceptRows = 1024;    // rows per request of a forced (prefill) commit
 constexpr int kRowMaxQuadsPerThread = 4;  // widths up to 16384
-// Polls of the fused quantisation's release word (each an atomic round trip plus a short sleep)
-// before it gives up and reports a fault: far beyond any real wait.
-constexpr int kFusedQuantizeSpins = 1 << 17;
 
 __device__ __forceinline__ float inverse_rms(float square_sum, int width, float eps) {
   return rsqrtf(square_sum / static_cast<float>(width) + eps);
@@ -229,52 +226,12 @@ __global__ __launch_bounds__(kThreads) void layer_end_kernel(const RowArgs a) {
     return;
   }
 
-  // ---- fused e4m3 quantisation of y. Every workgroup publishes its amax (a returning atomic,
-  // complete before the arrival), then arrives; the last to arrive reads every stripe and
-  // releases the tensor's amax; the others wait for the release. Agent-scope read-modify-writes
-  // are coherent across the XCDs without cache maintenance, so no fence is needed: the only
-  // values exchanged are these atomics.
+  // ---- fused e4m3 quantisation of y: the workgroups agree on the tensor's amax, then each
+  // quantises its own row.
   __shared__ float tensor_amax;
   if (threadIdx.x < kWave) {
-    const int lane = threadIdx.x;
-    unsigned *release = a.sync + kAmaxStripeFloats;
-    int last = 0;
-    if (lane == 0) {
-      unsigned *stripe = reinterpret_cast<unsigned *>(a.y_amax) +
-                         (blockIdx.x % a.amax_stripes) * kAmaxStripeFloats;
-      const unsigned before = __hip_atomic_fetch_max(stripe, __float_as_uint(amax), __ATOMIC_RELAXED,
-                                                     __HIP_MEMORY_SCOPE_AGENT);
-      __asm__ volatile("s_waitcnt vmcnt(0)" ::"v"(before) : "memory");
-      const unsigned arrived =
-          __hip_atomic_fetch_add(a.sync, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      last = arrived + 1 == gridDim.x;
-    }
-    last = __shfl(last, 0, kWave);
-    float total;
-    if (last) {
-      const unsigned bits = lane < a.amax_stripes
-                                ? __hip_atomic_fetch_max(reinterpret_cast<unsigned *>(a.y_amax) +
-                                                             lane * kAmaxStripeFloats,
-                                                         0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                                : 0u;
-      total = wave_max(__uint_as_float(bits));
-      if (lane == 0)
-        (void)__hip_atomic_exchange(release, __float_as_uint(total) | 0x80000000u,
-                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    } else {
-      unsigned seen = 0;
-      if (lane == 0) {
-        for (int spin = 0; spin < kFusedQuantizeSpins; ++spin) {
-          seen = __hip_atomic_fetch_or(release, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          if (seen & 0x80000000u) break;
-          __builtin_amdgcn_s_sleep(2);
-        }
-        if (!(seen & 0x80000000u))
-          (void)__hip_atomic_fetch_or(a.fault, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-      total = __uint_as_float(__shfl(static_cast<int>(seen & 0x7fffffffu), 0, kWave));
-    }
-    if (lane == 0) tensor_amax = total;
+    const float total = fused_amax_release(a.y_amax, a.amax_stripes, a.sync, a.fault, gridDim.x, amax);
+    if (threadIdx.x == 0) tensor_amax = total;
   }
   __syncthreads();
   const float q_inv = 1.0f / fp8_scale_from_amax(tensor_amax);

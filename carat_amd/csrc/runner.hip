@@ -283,6 +283,12 @@ struct BatchModelRunner::Implementation {
     probe_used = 0;
   }
 
+  void set_fused_quantization(bool enabled) {
+    fused_quantize_enabled = enabled;
+    for (auto &entry : verify_graphs) (void)hipGraphExecDestroy(entry.second);
+    verify_graphs.clear();  // captured steps hold the previous choice
+  }
+
   void release_handles() {
     for (auto &entry : probe_pool) {
       (void)hipEventDestroy(entry.first);
@@ -1942,6 +1948,9 @@ void *BatchModelRunner::tensor(const std::string &name, size_t *bytes,
 }
 hipStream_t BatchModelRunner::stream() const { return implementation_->stream; }
 void BatchModelRunner::set_graphs_enabled(bool enabled) { implementation_->graphs_enabled = enabled; }
+void BatchModelRunner::set_fused_quantization(bool enabled) {
+  implementation_->set_fused_quantization(enabled);
+}
 float BatchModelRunner::last_verify_ms() const { return implementation_->verify_ms; }
 float BatchModelRunner::last_draft_ms() const { return implementation_->draft_ms; }
 void BatchModelRunner::set_probe(int kind) {

@@ -163,6 +163,37 @@ def test_graph_replay_matches_eager(model):
         runner.set_graphs(False)
 
 
+def fused_and_separate_quantization(runner, props, first, slots, names):
+    """One dry verify with the producers quantising the next GEMM's operand themselves, one with
+    the separate quantisation kernel: predictions and the named tensors of both."""
+    out = []
+    for fused in (True, False):
+        runner.set_fused_quantization(fused)
+        try:
+            runner.verify_greedy_proposals(props, first, slots, [0] * len(slots))
+            out.append((list(runner.last_predictions), [runner.read(n, np.uint16).copy() for n in names]))
+        finally:
+            runner.set_fused_quantization(True)
+    return out
+
+
+def test_fused_quantization_equals_the_separate_kernel(model):
+    """The layer-end rows quantise the next GEMM's e4m3 operand themselves (a grid-wide amax
+    agreement first); the result must equal the separate prepare kernel's bit for bit (same
+    rounding of the same bf16 values with the same per-tensor scale)."""
+    desc, runner = model
+    reset_state(runner, [40, 55, 70, 90], seed=13)
+    rng = np.random.default_rng(21)
+    props = rng.integers(0, desc.vocabulary, (4, 5)).tolist()
+    first = [p[0] for p in props]
+    say("case: fused vs separate activation quantisation, tiny model")
+    names = ["final_hidden"] + [f"new.{li}.k" for li in range(len(desc.layers))]
+    (p_fused, t_fused), (p_sep, t_sep) = fused_and_separate_quantization(runner, props, first, [0, 1, 2, 3], names)
+    assert p_fused == p_sep
+    for name, a, b in zip(names, t_fused, t_sep):
+        assert np.array_equal(a, b), name
+
+
 def test_reference_error_messages(model):
     desc, runner = model
     reset_state(runner, [10, 10, 10, 0])
