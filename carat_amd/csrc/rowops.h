@@ -49,8 +49,8 @@ struct RowArgs {
   // quantised to e4m3 with its per-tensor scale (amax / 448), in the fp8 GEMM's activation
   // operand order (gemm.hip prepare_x_kernel's layout, xprep_token_tiles tiles per token block),
   // so no separate quantisation kernel runs. The workgroups agree on the amax through `sync`
-  // (two zeroed words, kAmaxStripeFloats floats apart: an arrival counter and the released
-  // amax); a wait that exceeds its bound sets *fault and the output is not to be used.
+  // (kFusedSyncWords zeroed words, kAmaxStripeFloats floats apart: arrival counters and the
+  // released amax); a wait that exceeds its bound sets *fault and the output is not to be used.
   unsigned char *xprep = nullptr;
   int xprep_token_tiles = 8;
   unsigned *sync = nullptr;

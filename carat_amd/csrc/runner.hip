@@ -56,6 +56,7 @@ constexpr int kMaximumDepth = 8;  // batch_model_runner.cu:33 speculative_depth
 constexpr int kPrefillStepRows = 1024;
 constexpr int kAmaxStripes = 64;  // stripes per per-tensor amax (see amax_publish)
 constexpr int kAmaxSlotFloats = kAmaxStripes * kAmaxStripeFloats;  // storage per amax
+static_assert(kAmaxStripes >= kFusedSyncWords, "a sync slot holds the fused quantisation's words");
 
 class DeviceBuffer {
 public:
