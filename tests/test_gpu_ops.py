@@ -362,7 +362,8 @@ def test_deep_prefill_step_attention(dev, chunk):
     assert attention_err(got, oracle.verify_attention(q, kc, vc, kn, vn, slots, positions, C, 0)) <= 2e-2
 
 
-@pytest.mark.parametrize("chunk", [0, 256])
+# 0: one workgroup per pair; 256 / 512: five / three key chunks per pair and the merge
+@pytest.mark.parametrize("chunk", [0, 256, 512])
 def test_sliding_verify_attention_config2(dev, chunk):
     """Config 2: 24 slots, T=5, 32/16 heads x 128, ring 1024, contexts U[256, 8192] (mixed
     wrapped / unwrapped slots in one launch)."""
