@@ -182,6 +182,7 @@ struct BatchModelRunner::Implementation {
     if (p != nullptr) (void)hipHostFree(p);
   }};
   int last_rows = 0;  // rows of the last verify step (the stream probe's activation shape)
+  int last_requests = 0, last_depth = 0;
   std::vector<std::pair<hipEvent_t, hipEvent_t>> probe_pool;
   size_t probe_used = 0;
   double probe_total_ms = 0.0;
@@ -765,13 +766,19 @@ struct BatchModelRunner::Implementation {
   // Back-to-back launches of one per-layer fp8 GEMM kind over every layer (see the header).
   float stream_gemm_probe(int kind, int passes, int *launches) {
     if (last_rows <= 0) throw std::runtime_error("stream probe needs a verify call first");
-    if (passes <= 0 || kind < probe_qkv_gemm || kind > probe_down_gemm)
+    const bool attention = kind == probe_sliding_attention || kind == probe_global_attention;
+    if (passes <= 0 || ((kind < probe_qkv_gemm || kind > probe_down_gemm) && !attention))
       throw std::runtime_error("invalid stream probe");
     const int rows = last_rows;
     auto launch = [&](size_t li, bool prepared) {
       TargetLayer &L = layers[li];
       const float *scales = L.scales.as<float>();
       switch (kind) {
+      case probe_sliding_attention:
+      case probe_global_attention:
+        if (L.spec.sliding == (kind == probe_sliding_attention))
+          launch_attention(layer_attention(li, last_requests, last_depth, d_positions, d_slots), stream);
+        break;
       case probe_qkv_gemm:
         run_fp8_gemm(normalized.as<bf16_t>(), rows, spec.hidden, amax_slot(li, 0), L.qkv, scales + 0,
                      GemmEpilogue::partial_f32, nullptr, nullptr, nullptr, probe_none, prepared);
@@ -793,7 +800,7 @@ struct BatchModelRunner::Implementation {
         break;
       }
     };
-    launch(0, false);  // prepares the activation operand once
+    if (!attention) launch(0, false);  // prepares the activation operand once
     hipEvent_t start, stop;
     hip_check(hipEventCreate(&start), "create probe event");
     hip_check(hipEventCreate(&stop), "create probe event");
@@ -806,7 +813,13 @@ struct BatchModelRunner::Implementation {
     hip_check(hipEventElapsedTime(&ms, start, stop), "probe time");
     hip_check(hipEventDestroy(start), "destroy probe event");
     hip_check(hipEventDestroy(stop), "destroy probe event");
-    *launches = passes * static_cast<int>(layers.size());
+    size_t per_pass = layers.size();
+    if (attention) {
+      per_pass = 0;
+      for (auto &L : layers) per_pass += L.spec.sliding == (kind == probe_sliding_attention) ? 1 : 0;
+      if (per_pass == 0) throw std::runtime_error("stream probe: the model has no layer of that kind");
+    }
+    *launches = passes * static_cast<int>(per_pass);
     return ms / static_cast<float>(*launches);
   }
 
@@ -824,6 +837,37 @@ struct BatchModelRunner::Implementation {
     bool fused_quantize = false;
     bool input_prepared = false;  // the xprep workspace already holds `normalized`, quantised
   };
+
+  // Verify attention of layer li over one step's rows (queries, this step's K/V rows and the
+  // layer's cache; output and its amax into the step's buffers).
+  AttentionArgs layer_attention(size_t li, int requests, int depth, const int32_t *positions,
+                                const int32_t *slots) {
+    TargetLayer &L = layers[li];
+    AttentionArgs at;
+    at.amax_stripes = kAmaxStripes;
+    at.mode = L.spec.sliding ? AttentionMode::sliding : AttentionMode::global;
+    at.q = queries.as<bf16_t>();
+    at.k_cache = L.k_cache.get();
+    at.v_cache = L.v_cache.get();
+    at.k_new = L.k_new.get();
+    at.v_new = L.v_new.get();
+    at.slots = slots;
+    at.slot_count = batch_size;
+    at.positions = positions;
+    at.requests = requests;
+    at.tokens = depth;
+    at.query_heads = L.spec.query_heads;
+    at.kv_heads = L.spec.kv_heads;
+    at.dimension = L.spec.head_dimension;
+    at.capacity = L.capacity;
+    at.window = std::min(spec.sliding_window, L.capacity);
+    at.max_keys = L.spec.sliding ? at.window + depth - 1 : maximum_context;
+    at.out = attention_out.as<bf16_t>();
+    at.out_amax = amax_slot(li, 1);
+    at.partials = attention_partials.as<float>();
+    at.chunk_keys = L.spec.sliding ? attention_chunk_sliding : attention_chunk_global;
+    return at;
+  }
 
   // Layer li over one step's rows: QKV projection and post-processing (global rows go straight to
   // the cache, sliding rows to the layer's k_new/v_new for the commit), attention, O projection,
@@ -879,29 +923,7 @@ struct BatchModelRunner::Implementation {
       q.capacity = L.capacity;
     }
     launch_qkv_post(q, stream);
-    AttentionArgs at;
-    at.amax_stripes = kAmaxStripes;
-    at.mode = L.spec.sliding ? AttentionMode::sliding : AttentionMode::global;
-    at.q = queries.as<bf16_t>();
-    at.k_cache = L.k_cache.get();
-    at.v_cache = L.v_cache.get();
-    at.k_new = L.k_new.get();
-    at.v_new = L.v_new.get();
-    at.slots = io.slots;
-    at.slot_count = batch_size;
-    at.positions = io.positions;
-    at.requests = io.requests;
-    at.tokens = io.depth;
-    at.query_heads = L.spec.query_heads;
-    at.kv_heads = L.spec.kv_heads;
-    at.dimension = D;
-    at.capacity = L.capacity;
-    at.window = std::min(spec.sliding_window, L.capacity);
-    at.max_keys = L.spec.sliding ? at.window + io.depth - 1 : maximum_context;
-    at.out = attention_out.as<bf16_t>();
-    at.out_amax = amax_slot(li, 1);
-    at.partials = attention_partials.as<float>();
-    at.chunk_keys = L.spec.sliding ? attention_chunk_sliding : attention_chunk_global;
+    AttentionArgs at = layer_attention(li, io.requests, io.depth, io.positions, io.slots);
     std::tie(at.timing_start, at.timing_stop) =
         probe(L.spec.sliding ? probe_sliding_attention : probe_global_attention);
     launch_attention(at, stream);
@@ -1009,6 +1031,8 @@ struct BatchModelRunner::Implementation {
                       bool lm_head_pass = true) {
     const int rows = requests * depth;
     last_rows = rows;
+    last_requests = requests;
+    last_depth = depth;
     launch_step_init(amax.as<float>(), static_cast<int>(amax_slot_count() * kAmaxStripes), stream,
                      d_fault);
     enqueue_embedding(d_tokens, rows, hidden_a.as<bf16_t>(), normalized.as<bf16_t>(),

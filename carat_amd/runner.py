@@ -322,7 +322,8 @@ class BatchModelRunner:
         return total.value, launches.value
 
     def stream_gemm_probe(self, kind: str, passes: int = 1) -> tuple[float, int]:
-        """Mean ms per launch of one per-layer GEMM kind, launched back to back over every layer."""
+        """Mean ms per launch of one per-layer kernel kind (an fp8 GEMM or the sliding / global
+        verify attention), launched back to back over every layer that has it."""
         avg = ctypes.c_float()
         launches = ctypes.c_int()
         check(lib().carat_hip_runner_stream_gemm_probe(self._handle, self.PROBES[kind], passes,

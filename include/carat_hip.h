@@ -220,10 +220,12 @@ int carat_hip_bench_speculative_cycle(carat_hip_runner *runner, int requests, in
  * -1 off). Probing runs the verify step without HIP graphs. read_probe returns and resets the sums. */
 int carat_hip_runner_set_probe(carat_hip_runner *runner, int kind);
 int carat_hip_runner_read_probe(carat_hip_runner *runner, float *total_ms, int *launches);
-/* Benchmark probe, no counterpart in the reference: back-to-back launches of one per-layer fp8 GEMM
- * kind (0 qkv, 1 O, 2 gate/up, 3 down) over every layer's weights, `passes` times, on the last
- * verify's activations, timed with one pair of hip events; *avg_ms = mean time per launch. Only
- * that GEMM's scratch outputs are overwritten. */
+/* Benchmark probe, no counterpart in the reference: back-to-back launches of one per-layer kernel
+ * kind over every layer of the model that has it, `passes` times, on the last verify's
+ * activations, timed with one pair of hip events; *avg_ms = mean time per launch. Kinds: fp8 GEMMs
+ * 0 qkv, 1 O, 2 gate/up, 3 down (every layer's weights); 5 sliding and 6 global verify attention
+ * (every such layer's cache, with its K/V rows of the last step). Only that kernel's scratch
+ * outputs are overwritten. */
 int carat_hip_runner_stream_gemm_probe(carat_hip_runner *runner, int kind, int passes,
                                        float *avg_ms, int *launches);
 

@@ -317,6 +317,9 @@ def test_stream_gemm_probe_leaves_the_verify_result_unchanged(model):
     for kind in ("qkv_gemm", "o_gemm", "gate_up_gemm", "down_gemm"):
         avg_ms, launches = runner.stream_gemm_probe(kind, passes=2)
         assert launches == 2 * len(desc.layers) and avg_ms > 0.0
+    for kind, sliding in (("sliding_attention", True), ("global_attention", False)):
+        avg_ms, launches = runner.stream_gemm_probe(kind, passes=2)
+        assert launches == 2 * sum(l.sliding == sliding for l in desc.layers) and avg_ms > 0.0
     runner.verify_greedy_proposals(props, first, slots, [0] * 4)
     assert runner.last_predictions == before
 
