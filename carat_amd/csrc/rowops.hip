@@ -608,7 +608,8 @@ bool launch_layer_end(const RowArgs &a, hipStream_t stream) {
   const bool fixed = a.source == RowSource::partials && (scaled || (a.x_amax == nullptr && a.w_scale == nullptr)) &&
                      a.w1 != nullptr && a.residual != nullptr && a.r1_out != nullptr &&
                      a.w2 != nullptr && a.y_out != nullptr && (a.y_amax != nullptr || !scaled) &&
-                     a.v_out == nullptr && a.rows < 512 && a.splits >= 1 && a.splits <= 4;
+                     a.v_out == nullptr && a.rows < 512 &&
+                     ((a.splits >= 1 && a.splits <= 4) || a.splits == 8);
   const int quads = a.width / 4;
   // (quads per thread, threads): 5376 wide rows take 448 x 3 with no idle lane
   const int q = a.width == 5376 ? 3 : quads <= 256 ? 5 : quads <= 1024 ? 1 : quads <= 2048 ? 2 : quads <= 4096 ? 4 : 0;
@@ -627,7 +628,8 @@ bool launch_layer_end(const RowArgs &a, hipStream_t stream) {
       case 1: layer_end_kernel<Q, T, 1, S><<<a.rows, T, 0, stream>>>(a); break;
       case 2: layer_end_kernel<Q, T, 2, S><<<a.rows, T, 0, stream>>>(a); break;
       case 3: layer_end_kernel<Q, T, 3, S><<<a.rows, T, 0, stream>>>(a); break;
-      default: layer_end_kernel<Q, T, 4, S><<<a.rows, T, 0, stream>>>(a); break;
+      case 4: layer_end_kernel<Q, T, 4, S><<<a.rows, T, 0, stream>>>(a); break;
+      default: layer_end_kernel<Q, T, 8, S><<<a.rows, T, 0, stream>>>(a); break;  // the assistant's down
       }
     };
     if (scaled) pick(std::true_type{}); else pick(std::false_type{});
