@@ -992,15 +992,17 @@ int attention_default_chunk(AttentionMode mode, int max_keys, int requests, int 
   // sliding verify 50 us whole, 54 us in two chunks plus the merge). Smaller batches split the
   // range so that up to 512 workgroups stream it.
   //
-  // e4m3 K/V at D = 128 is the exception: a workgroup moves half the bytes per key, and with one
-  // workgroup per pair the 128 CUs holding two of them fall behind the 128 holding one (cold
-  // HBM, 24 x 16 pairs x 8155 keys: the single-workgroup CUs finish 134 us in, the last
-  // workgroups at 182 us). Two chunks per pair put exactly three workgroups on every CU
-  // (768 workgroups at three per CU): 152 us plus the merge.
+  // Two exceptions at D = 128, where three workgroups fit a CU: with one workgroup per pair the
+  // 128 CUs holding two of them fall behind the 128 holding one, and two chunks per pair put
+  // exactly three workgroups on every CU (768 workgroups). e4m3 K/V verify (a workgroup moves
+  // half the bytes per key; cold HBM, 24 x 16 pairs x 8155 keys: the single-workgroup CUs finish
+  // 134 us in, the last workgroups at 182 us; two chunks: 152 us plus the merge), and the
+  // assistant's decode over the global cache (one query row per head, no amax for the merge to
+  // publish: 3.31 -> 3.26 ms per draft). bf16 verify gains nothing from it (13.61 ms either way).
   const int whole = ((max_keys + 255) / 256) * 256;
   const int pairs = std::max(1, requests * kv_heads);
-  if (fp8_kv && mode != AttentionMode::decode && dimension == 128 && pairs >= 256 &&
-      2 * pairs <= 3 * 256 && max_keys >= 2048)
+  const bool balance = (fp8_kv && mode != AttentionMode::decode) || (!fp8_kv && mode == AttentionMode::decode);
+  if (balance && dimension == 128 && pairs >= 256 && 2 * pairs <= 3 * 256 && max_keys >= 2048)
     return ((max_keys + 1) / 2 + 255) / 256 * 256;
   if (pairs >= 256) return whole;
   // the smallest 256-key multiple that keeps the workgroups at <= 512

@@ -116,6 +116,7 @@ struct AssistantLayer {
   bool global = false;
   int kv_heads = 0;
   int head_dimension = 0;
+  int attention_chunk = 0;  // keys per workgroup of its decode attention over the target cache
   DeviceBuffer input_norm, q_norm, post_attention_norm, pre_mlp_norm, post_mlp_norm, scalar;
   PackedWeight q, o, gate_up, down;  // bf16
 };
@@ -664,10 +665,11 @@ struct BatchModelRunner::Implementation {
     if (has_assistant)
       for (auto &L : assistant_layers) {
         const TargetLayer &target = layers[static_cast<size_t>(L.global ? last_global : last_sliding)];
-        const int chunk = target.spec.sliding ? attention_chunk_sliding : attention_chunk_global;
+        L.attention_chunk = attention_default_chunk(AttentionMode::decode, target.capacity, batch_size,
+                                                    L.kv_heads, false, L.head_dimension);
         attention_partial_floats = std::max(
             attention_partial_floats,
-            attention_partials_floats(batch_size, L.kv_heads, target.capacity, chunk,
+            attention_partials_floats(batch_size, L.kv_heads, target.capacity, L.attention_chunk,
                                       spec.assistant.query_heads / L.kv_heads, L.head_dimension));
       }
     attention_partials.allocate(sizeof(float) * attention_partial_floats);
@@ -1555,7 +1557,7 @@ struct BatchModelRunner::Implementation {
     at.max_keys = target.capacity;
     at.out = a_attention_out.as<bf16_t>();
     at.partials = attention_partials.as<float>();
-    at.chunk_keys = target.spec.sliding ? attention_chunk_sliding : attention_chunk_global;
+    at.chunk_keys = L.attention_chunk;
     launch_attention(at, stream);
     splits = run_bf16_gemm_partial(a_attention_out.as<bf16_t>(), active, qw, L.o);
     RowArgs ro;
