@@ -583,7 +583,7 @@ int carat_hip_runner_set_graphs(carat_hip_runner *runner, int enabled) {
 }
 
 int carat_hip_runner_set_fused_quantization(carat_hip_runner *runner, int enabled) {
-  return guarded([&] { runner_of(runner).set_fused_quantization(enabled != 0); });
+  return guarded([&] { runner_of(runner).set_fused_quantization(enabled); });
 }
 int carat_hip_runner_set_probe(carat_hip_runner *runner, int kind) {
   return guarded([&] { runner_of(runner).set_probe(kind); });

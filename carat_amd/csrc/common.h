@@ -194,14 +194,15 @@ __device__ __forceinline__ float amax_read(const float *amax, int stripes) {
 // coherent across the XCDs without cache maintenance, so no fence is needed: the only values
 // exchanged are these atomics. `sync` holds kFusedSyncWords words kAmaxStripeFloats floats apart
 // (global counter, release word, eight counters), zeroed beforehand; `workgroups` is the number
-// that arrive. A wait past kFusedQuantizeSpins polls sets *fault (the result is then not to be
-// used) and returns. The arriving workgroups must be resident at once, or the early ones wait
+// that arrive. A wait past `spins` polls (kFusedQuantizeSpins in production, far beyond any real
+// wait) sets *fault (the result is then not to be used) and returns. The arriving workgroups must be resident at once, or the early ones wait
 // for the bound.
 constexpr int kFusedQuantizeSpins = 1 << 17;
 constexpr int kFusedSyncWords = 10;
 __device__ __forceinline__ float fused_amax_release(float *amax, int stripes, unsigned *sync,
                                                     int32_t *fault, unsigned workgroups,
-                                                    float workgroup_amax) {
+                                                    float workgroup_amax,
+                                                    int spins = kFusedQuantizeSpins) {
   const int lane = threadIdx.x & (kWave - 1);
   unsigned *release = sync + kAmaxStripeFloats;
   const unsigned flat = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
@@ -233,7 +234,7 @@ __device__ __forceinline__ float fused_amax_release(float *amax, int stripes, un
   }
   unsigned seen = 0;
   if (lane == 0) {
-    for (int spin = 0; spin < kFusedQuantizeSpins; ++spin) {
+    for (int spin = 0; spin < spins; ++spin) {
       seen = __hip_atomic_fetch_or(release, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       if (seen & 0x80000000u) break;
       __builtin_amdgcn_s_sleep(2);

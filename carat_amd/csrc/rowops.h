@@ -55,6 +55,7 @@ struct RowArgs {
   int xprep_token_tiles = 8;
   unsigned *sync = nullptr;
   int32_t *fault = nullptr;
+  int quantize_spins = kFusedQuantizeSpins;  // bound of a wait for the agreed amax (0: no wait)
 };
 constexpr int kFusedQuantizeRows = 192;  // every row's workgroup is resident at once (256 CUs)
 void launch_row_kernel(const RowArgs &args, hipStream_t stream);

@@ -230,7 +230,8 @@ __global__ __launch_bounds__(kThreads) void layer_end_kernel(const RowArgs a) {
   // quantises its own row.
   __shared__ float tensor_amax;
   if (threadIdx.x < kWave) {
-    const float total = fused_amax_release(a.y_amax, a.amax_stripes, a.sync, a.fault, gridDim.x, amax);
+    const float total = fused_amax_release(a.y_amax, a.amax_stripes, a.sync, a.fault, gridDim.x, amax,
+                                           a.quantize_spins);
     if (threadIdx.x == 0) tensor_amax = total;
   }
   __syncthreads();

@@ -160,10 +160,11 @@ public:
   hipStream_t stream() const;
   // Optional HIP-graph replay of the verify step (keyed by batch shape).
   void set_graphs_enabled(bool enabled);
-  // Whether the verify step's activation producers (layer-end rows, gate/up) quantise the next
-  // GEMM's operand themselves (default) or a separate prepare kernel does; the results are the
-  // same bit for bit.
-  void set_fused_quantization(bool enabled);
+  // Whether the verify step's layer-end rows quantise the next GEMM's operand themselves (1, the
+  // default) or a separate prepare kernel does (0); the results are the same bit for bit. 2 fuses
+  // with a zero bound on the workgroups' wait for the agreed amax, so that every waiting
+  // workgroup reports a timeout and the step raises (a test of that error path).
+  void set_fused_quantization(int mode);
   // Milliseconds of the last verify / draft call's device work (hip events on the runner stream).
   float last_verify_ms() const;
   float last_draft_ms() const;

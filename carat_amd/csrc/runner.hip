@@ -210,7 +210,7 @@ struct BatchModelRunner::Implementation {
           *d_fault = nullptr;
   int32_t *host_io = nullptr;  // pinned mirror of device_io
   // verify steps quantise the layer-end rows' outputs in the row kernels (RowArgs::xprep)
-  bool fused_quantize_enabled = true;
+  int fused_quantize_mode = 1;  // 0 off, 1 on, 2 on with a zero wait bound (error-path test)
   bool last_input_prepared = false;
   size_t io_ints = 0;
   int sliding_layer_count = 0;
@@ -286,8 +286,9 @@ struct BatchModelRunner::Implementation {
     probe_used = 0;
   }
 
-  void set_fused_quantization(bool enabled) {
-    fused_quantize_enabled = enabled;
+  void set_fused_quantization(int mode) {
+    if (mode < 0 || mode > 2) throw std::runtime_error("fused quantisation mode must be 0, 1 or 2");
+    fused_quantize_mode = mode;
     for (auto &entry : verify_graphs) (void)hipGraphExecDestroy(entry.second);
     verify_graphs.clear();  // captured steps hold the previous choice
   }
@@ -886,6 +887,7 @@ struct BatchModelRunner::Implementation {
       r.xprep_token_tiles = gemm_token_tiles(rows);
       r.sync = sync_slot(li, which);
       r.fault = d_fault;
+      r.quantize_spins = fused_quantize_mode == 2 ? 0 : kFusedQuantizeSpins;
     };
     TargetLayer &L = layers[li];
     const float *scales = L.scales.as<float>();
@@ -1047,7 +1049,7 @@ struct BatchModelRunner::Implementation {
     io.input = hidden_a.as<bf16_t>();
     io.output = hidden_b.as<bf16_t>();
     io.normalized = normalized.as<bf16_t>();
-    io.fused_quantize = fused_quantize_enabled;
+    io.fused_quantize = fused_quantize_mode != 0;
     for (size_t li = 0; li < layers.size(); ++li) {
       io.in_amax = amax_slot(li, 0);
       const bool last = li + 1 == layers.size();
@@ -1975,8 +1977,8 @@ void *BatchModelRunner::tensor(const std::string &name, size_t *bytes,
 }
 hipStream_t BatchModelRunner::stream() const { return implementation_->stream; }
 void BatchModelRunner::set_graphs_enabled(bool enabled) { implementation_->graphs_enabled = enabled; }
-void BatchModelRunner::set_fused_quantization(bool enabled) {
-  implementation_->set_fused_quantization(enabled);
+void BatchModelRunner::set_fused_quantization(int mode) {
+  implementation_->set_fused_quantization(mode);
 }
 float BatchModelRunner::last_verify_ms() const { return implementation_->verify_ms; }
 float BatchModelRunner::last_draft_ms() const { return implementation_->draft_ms; }

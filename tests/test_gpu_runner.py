@@ -194,6 +194,33 @@ def test_fused_quantization_equals_the_separate_kernel(model):
         assert np.array_equal(a, b), name
 
 
+def test_fused_quantization_wait_timeout_is_an_error(model):
+    """A layer-end workgroup whose wait for the agreed amax runs out sets a fault flag; the step
+    raises instead of returning results from a partly quantised operand. Forced from the host with
+    a zero wait bound (every waiting workgroup gives up at once, so no kernel ever spins); the
+    next step runs normally, and a dry step leaves no state behind."""
+    desc, runner = model
+    reset_state(runner, [33, 47, 61, 75], seed=14)
+    rng = np.random.default_rng(22)
+    props = rng.integers(0, desc.vocabulary, (4, 5)).tolist()
+    first = [p[0] for p in props]
+    slots = [0, 1, 2, 3]
+    say("case: fused quantisation wait bound of zero")
+    runner.verify_greedy_proposals(props, first, slots, [0] * 4)
+    before = list(runner.last_predictions)
+    with pytest.raises(CaratError, match="fused activation quantisation timed out"):
+        runner.set_fused_quantization(2)
+        try:
+            runner.verify_greedy_proposals(props, first, slots, [0] * 4)
+        finally:
+            runner.set_fused_quantization(1)
+    with pytest.raises(CaratError, match="fused quantisation mode"):
+        runner.set_fused_quantization(3)
+    runner.verify_greedy_proposals(props, first, slots, [0] * 4)
+    assert runner.last_predictions == before
+    assert [runner.slot_position(s) for s in slots] == [33, 47, 61, 75]
+
+
 def test_reference_error_messages(model):
     desc, runner = model
     reset_state(runner, [10, 10, 10, 0])
