@@ -160,8 +160,9 @@ public:
   hipStream_t stream() const;
   // Optional HIP-graph replay of the verify step (keyed by batch shape).
   void set_graphs_enabled(bool enabled);
-  // Whether the verify step's layer-end rows quantise the next GEMM's operand themselves (1, the
-  // default) or a separate prepare kernel does (0); the results are the same bit for bit. 2 fuses
+  // Whether the verify step's layer-end rows quantise the next GEMM's operand themselves (1) or a
+  // separate prepare kernel does (0, the default: faster in the step); the results are the same
+  // bit for bit. 2 fuses
   // with a zero bound on the workgroups' wait for the agreed amax, so that every waiting
   // workgroup reports a timeout and the step raises (a test of that error path).
   void set_fused_quantization(int mode);

@@ -210,7 +210,9 @@ struct BatchModelRunner::Implementation {
           *d_fault = nullptr;
   int32_t *host_io = nullptr;  // pinned mirror of device_io
   // verify steps quantise the layer-end rows' outputs in the row kernels (RowArgs::xprep)
-  int fused_quantize_mode = 1;  // 0 off, 1 on, 2 on with a zero wait bound (error-path test)
+  // 0 (default): separate prepare kernels, measured faster in the step than the fused
+  // quantisation (1); 2: fused with a zero wait bound (error-path test)
+  int fused_quantize_mode = 0;
   bool last_input_prepared = false;
   size_t io_ints = 0;
   int sliding_layer_count = 0;

@@ -307,7 +307,8 @@ class BatchModelRunner:
         check(lib().carat_hip_runner_set_graphs(self._handle, int(enabled)))
 
     def set_fused_quantization(self, mode: int) -> None:
-        """1 (default) fused, 0 separate kernel, 2 fused with a zero wait bound (error-path test)."""
+        """0 (default) separate quantisation kernel, 1 fused into the layer-end rows, 2 fused with a
+        zero wait bound (error-path test)."""
         check(lib().carat_hip_runner_set_fused_quantization(self._handle, int(mode)))
 
     PROBES = {"qkv_gemm": 0, "o_gemm": 1, "gate_up_gemm": 2, "down_gemm": 3, "lm_head_gemm": 4,

@@ -199,8 +199,8 @@ int carat_hip_runner_tensor(carat_hip_runner *runner, const char *name, void **d
 int carat_hip_runner_copy_tensor(carat_hip_runner *runner, const char *name, void *host,
                                  size_t bytes, int direction);
 int carat_hip_runner_set_graphs(carat_hip_runner *runner, int enabled);
-/* 1 (default): the verify step's layer-end rows write the next fp8 GEMM's operand themselves;
- * 0: a separate quantisation kernel does. Same results bit for bit. 2: fused with a zero bound
+/* 0 (default): a separate quantisation kernel prepares the next fp8 GEMM's operand; 1: the verify
+ * step's layer-end rows write it themselves. Same results bit for bit. 2: fused with a zero bound
  * on the workgroups' wait for the agreed amax, so the step reports the timeout error (a test of
  * that path). Other values are rejected. */
 int carat_hip_runner_set_fused_quantization(carat_hip_runner *runner, int enabled);

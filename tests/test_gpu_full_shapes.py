@@ -251,7 +251,7 @@ def test_config5_fused_quantization_equals_the_separate_kernel(full_model):
             assert res.accepted_tokens == [0] * SLOTS
             out.append((list(runner.last_predictions), [runner.read(n, np.uint16).copy() for n in names]))
         finally:
-            runner.set_fused_quantization(True)
+            runner.set_fused_quantization(0)
     assert out[0][0] == out[1][0]
     for name, a, b in zip(names, out[0][1], out[1][1]):
         assert np.array_equal(a, b), name

@@ -173,7 +173,7 @@ def fused_and_separate_quantization(runner, props, first, slots, names):
             runner.verify_greedy_proposals(props, first, slots, [0] * len(slots))
             out.append((list(runner.last_predictions), [runner.read(n, np.uint16).copy() for n in names]))
         finally:
-            runner.set_fused_quantization(True)
+            runner.set_fused_quantization(0)
     return out
 
 
@@ -213,7 +213,7 @@ def test_fused_quantization_wait_timeout_is_an_error(model):
         try:
             runner.verify_greedy_proposals(props, first, slots, [0] * 4)
         finally:
-            runner.set_fused_quantization(1)
+            runner.set_fused_quantization(0)
     with pytest.raises(CaratError, match="fused quantisation mode"):
         runner.set_fused_quantization(3)
     runner.verify_greedy_proposals(props, first, slots, [0] * 4)
