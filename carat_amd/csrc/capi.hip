@@ -53,7 +53,10 @@ struct OpWorkspace {
   size_t xprep_bytes = 0;
   void *packed_weight = nullptr;  // the row-major weight of a standalone linear, packed
   size_t packed_weight_bytes = 0;
+  void *amax = nullptr;           // striped amax of a split attention call
+  size_t amax_bytes = 0;
 };
+constexpr int kOpAmaxStripes = 64;
 std::mutex workspace_mutex;
 std::map<int, OpWorkspace> workspaces;
 
@@ -817,7 +820,20 @@ int carat_hip_verify_attention(int mode, const uint16_t *q, const void *k_cache,
                                                      qrows, dimension),
            "allocate attention partials");
     a.partials = static_cast<float *>(w.partials);
-    launch_attention(a, static_cast<hipStream_t>(stream));
+    // A split range ends in a merge kernel whose workgroups all finish at once: their amax updates
+    // go to striped slots (zeroed first), folded into the caller's float afterwards, instead of
+    // queueing on one address.
+    const bool split = (max_keys + a.chunk_keys - 1) / a.chunk_keys > 1;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (split && out_amax != nullptr) {
+      ensure(w.amax, w.amax_bytes, sizeof(float) * kOpAmaxStripes * kAmaxStripeFloats,
+             "allocate attention amax stripes");
+      a.out_amax = static_cast<float *>(w.amax);
+      a.amax_stripes = kOpAmaxStripes;
+      launch_step_init(a.out_amax, kOpAmaxStripes, s);
+    }
+    launch_attention(a, s);
+    if (split && out_amax != nullptr) launch_amax_fold(a.out_amax, kOpAmaxStripes, out_amax, s);
   });
 }
 

@@ -98,6 +98,9 @@ void launch_qkv_post(const QkvArgs &args, hipStream_t stream);
 
 // Zeroes the stripes of `amax_count` per-step striped amaxes (stripe i at i * kAmaxStripeFloats).
 void launch_step_init(float *amax, int amax_count, hipStream_t stream, int32_t *flag = nullptr);
+// Folds a striped amax (`stripes` floats kAmaxStripeFloats apart) into one float with an atomic
+// max (the single-float form that op-level callers pass).
+void launch_amax_fold(const float *striped, int stripes, float *out, hipStream_t stream);
 
 // ---------------------------------------------------------------------------------------------
 // Acceptance + commit (cuda/batch_model_runner.cu:1735-1808, net effect of ops.cu:827-871).

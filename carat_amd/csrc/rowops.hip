@@ -718,6 +718,17 @@ void launch_qkv_post(const QkvArgs &a, hipStream_t stream) {
   hip_check(hipGetLastError(), "launch QKV post-processing");
 }
 
+__global__ __launch_bounds__(64) void amax_fold_kernel(const float *striped, int stripes, float *out) {
+  const float value = amax_read(striped, stripes);
+  if (threadIdx.x == 0) atomic_max_nonneg(out, value);
+}
+
+void launch_amax_fold(const float *striped, int stripes, float *out, hipStream_t stream) {
+  check_amax_stripes(stripes);
+  amax_fold_kernel<<<1, 64, 0, stream>>>(striped, stripes, out);
+  hip_check(hipGetLastError(), "launch amax fold");
+}
+
 void launch_step_init(float *amax, int amax_count, hipStream_t stream, int32_t *flag) {
   if (amax_count <= 0) return;
   step_init_kernel<<<(amax_count + 255) / 256, 256, 0, stream>>>(amax, amax_count, flag);
