@@ -234,6 +234,10 @@ int carat_hip_runner_stream_gemm_probe(carat_hip_runner *runner, int kind, int p
 /* ------------------------------------------------------------------------------------------ */
 /* op level (device pointers)                                                                   */
 /* ------------------------------------------------------------------------------------------ */
+/* The op-level calls keep their intermediates (argmax partial keys, the e4m3 activation operand,
+ * attention partials and amax stripes) in one workspace per device that the library owns and
+ * grows on demand (growing synchronises the device). Calls on one device therefore must not
+ * overlap: enqueue them on one stream, or synchronise between streams. */
 /* argmax_bf16_rows (cuda_ops.h, ops.cu:1566-1579) over fp32 (compared after bf16 rounding) or bf16
  * logits [requests*tokens][vocabulary], with the greedy acceptance of batch_model_runner.cu:
  * 1738-1759 fused (proposals nullable -> argmax only). caps nullable. */
