@@ -157,13 +157,14 @@ def full_model(torch_cuda):
     runner.close()
 
 
-def test_config5_verify_step_full_dimensions(full_model):
-    desc, runner, positions_by_slot = full_model
-    rng = np.random.default_rng(56)
-    slots = rng.permutation(SLOTS).astype(np.int32)
-    positions = positions_by_slot[slots]
-    first = rng.integers(0, VOCAB, SLOTS).astype(np.int32)
-    say("case: config-5 greedy chain (4 dry verifies)")
+def full_verify_case(runner, desc, slots, positions, first, depth, caps, rng, tag):
+    """One verify step of `depth` rows per slot at full dimensions against the oracle: plants the
+    target's greedy chain (dry verifies), rejects it at a seeded index in most slots, then checks
+    acceptance (with `caps`), predictions (near-ties only), this step's K/V rows, the final
+    hidden rows, the cache commit, the hidden hand-off and the positions."""
+    T = depth
+    M = SLOTS * T
+    say(f"case: {tag} greedy chain ({T} dry verifies)")
     chain = np.zeros((SLOTS, T + 1), np.int32)
     chain[:, 0] = first
     for t in range(T):
@@ -182,21 +183,25 @@ def test_config5_verify_step_full_dimensions(full_model):
     before = {li: (runner.read(f"cache.{li}.k", np.uint16), runner.read(f"cache.{li}.v", np.uint16))
               for li in (li_s, li_g)}
     hidden_before = runner.read("target_hidden", np.uint16).reshape(SLOTS, H).copy()
-    say("case: config-5 oracle verify step (CPU)")
+    say(f"case: {tag} oracle verify step (CPU)")
     expect = verify_step(runner, desc, SLOTS, capacity_of(desc), proposals, slots, positions)
-    say("case: config-5 runner verify")
-    res = runner.verify_greedy_proposals(proposals.tolist(), first.tolist(), slots.tolist())
+    say(f"case: {tag} runner verify")
+    if caps is None:
+        res = runner.verify_greedy_proposals(proposals.tolist(), first.tolist(), slots.tolist())
+    else:
+        res = runner.verify_greedy_proposals(proposals.tolist(), first.tolist(), slots.tolist(), caps.tolist())
     pred = np.array(runner.last_predictions, np.int32).reshape(SLOTS, T)
-    acc, nxt = oracle.greedy_accept(proposals, first, pred)
+    acc, nxt = oracle.greedy_accept(proposals, first, pred, caps)
     assert res.accepted_tokens == acc.tolist() and res.next_tokens == nxt.tolist()
-    for r in range(SLOTS):  # the planted pattern: accepted = first mismatching index
-        assert res.accepted_tokens[r] == (reject[r] if reject[r] < T else T)
+    for r in range(SLOTS):  # the planted pattern: accepted = first mismatching index, capped
+        want = reject[r] if reject[r] < T else T
+        assert res.accepted_tokens[r] == (want if caps is None else min(want, int(caps[r])))
     # predictions: near-ties only, mismatch rate reported
     logits = oracle.bf16_to_f32(expect["logits"]).astype(np.float64).reshape(M, -1)
     flat = pred.reshape(-1)
     gap = logits.max(1) - logits[np.arange(M), flat]
     mism = int(np.sum(flat != expect["predictions"]))
-    say(f"  config-5 argmax mismatches vs oracle {mism}/{M}, max gap {gap.max():.3e}")
+    say(f"  {tag} argmax mismatches vs oracle {mism}/{M}, max gap {gap.max():.3e}")
     assert np.all(gap <= 2 * 2 ** -7 * np.abs(logits).max(1))
     assert mism <= M // 10
     # this step's K/V rows and the final hidden rows
@@ -230,6 +235,31 @@ def test_config5_verify_step_full_dimensions(full_model):
         want = final_hidden[r * T + a - 1] if a > 0 else hidden_before[slot]
         assert np.array_equal(hidden_after[slot], want)
         assert runner.slot_position(int(slot)) == positions[r] + a
+
+
+def test_config5_verify_step_full_dimensions(full_model):
+    desc, runner, positions_by_slot = full_model
+    rng = np.random.default_rng(56)
+    slots = rng.permutation(SLOTS).astype(np.int32)
+    positions = positions_by_slot[slots]
+    first = rng.integers(0, VOCAB, SLOTS).astype(np.int32)
+    full_verify_case(runner, desc, slots, positions, first, T, None, rng, "config-5")
+
+
+def test_config5_depth8_verify_with_caps_full_dimensions(full_model):
+    """The deepest verify step (8 rows per slot, 192 rows) with per-slot caps
+    (batch_model_runner.h:56-60's maximum_accepted_tokens) at config-5 dimensions."""
+    desc, runner, _ = full_model
+    rng = np.random.default_rng(58)
+    depth = 8
+    positions = rng.integers(1024, MAX_CONTEXT - depth - 8, SLOTS).astype(np.int32)
+    for slot, p in enumerate(positions):
+        runner.set_slot_position(slot, int(p))
+    slots = rng.permutation(SLOTS).astype(np.int32)
+    positions = positions[slots]
+    first = rng.integers(0, VOCAB, SLOTS).astype(np.int32)
+    caps = rng.integers(0, depth + 1, SLOTS).astype(np.int32)
+    full_verify_case(runner, desc, slots, positions, first, depth, caps, rng, "depth-8 capped")
 
 
 def test_config5_fused_quantization_equals_the_separate_kernel(full_model):
