@@ -260,13 +260,13 @@ def test_fp8_lm_head_argmax_is_bit_exact_on_its_own_logits(dev):
 
 
 # 256 and 8192: 4-wave blocks of two tiles per wave; 21504 (the verify shape): 3-wave blocks of
-# four tiles per wave
-@pytest.mark.parametrize("inter", [256, 8192, 21504])
-def test_fp8_gelu_gate_epilogue(dev, inter):
+# four tiles per wave; at 1008 rows (a prefill step) eight token blocks, two workgroups per CU
+@pytest.mark.parametrize("inter,m", [(256, 120), (8192, 120), (21504, 120), (21504, 1008)])
+def test_fp8_gelu_gate_epilogue(dev, inter, m):
     torch = dev
     rng = np.random.default_rng(22)
-    m, k = 120, 512
-    say(f"case: fp8 gate/up + GELU epilogue inter={inter}")
+    k = 512
+    say(f"case: fp8 gate/up + GELU epilogue inter={inter} m={m}")
     x = oracle.f32_to_bf16(rng.standard_normal((m, k)))
     amax = float(np.abs(oracle.bf16_to_f32(x)).max())
     qw, sw = rand_fp8(rng, (2 * inter, k), 0.05)
