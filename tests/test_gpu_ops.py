@@ -239,10 +239,12 @@ def test_fp8_linear_matches_oracle(dev, m, k, n):
     assert np.allclose(summed, ref32, rtol=1e-3, atol=1e-4 * np.abs(ref32).max())
 
 
-def test_fp8_lm_head_argmax_is_bit_exact_on_its_own_logits(dev):
+# 120 x 8192: one-tile layout, one token block; 1008 x 32768: four-tile layout with eight token
+# blocks at two workgroups per CU (a prefill step whose prompt completes)
+@pytest.mark.parametrize("m,k,n", [(120, 1024, 8192), (1008, 512, 32768)])
+def test_fp8_lm_head_argmax_is_bit_exact_on_its_own_logits(dev, m, k, n):
     torch = dev
     rng = np.random.default_rng(21)
-    m, k, n = 120, 1024, 8192
     say(f"case: fp8 lm_head argmax m={m} k={k} n={n}")
     x = oracle.f32_to_bf16(rng.standard_normal((m, k)))
     amax = float(np.abs(oracle.bf16_to_f32(x)).max())
