@@ -12,10 +12,12 @@ the target's own greedy chain (computed untimed by dry verifies that commit noth
 draft matches with probability 0.7 (geometric acceptance), as config 5 specifies.
 
 Prints ONE JSON line. `value` = accepted tokens (sum of the reference's accepted_tokens, which
-counts the forced token, = emitted tokens per step) / timed seconds. `roofline` times the dominant
-kernel (the gate/up FP8 GEMM) after the timed steps: its launches over all 60 layers' weights run
-back to back on the runner's stream between one pair of HIP events (two passes, 120 launches), so
-the per-launch figure is kernel time as a profiler sees it, not event-marker overhead.
+counts the forced token, = emitted tokens per step) / timed seconds. `roofline` times the step's
+dominant kernel by total time, the global verify attention, after the timed steps: every global
+layer's attention over its own cache runs back to back on the runner's stream between one pair of
+HIP events (two passes), so the per-launch figure is kernel time as a profiler sees it, not
+event-marker overhead. `roofline_gate_up` (the largest GEMM), `roofline_attention_sliding` and
+`gemms` (every per-layer FP8 GEMM) are timed the same way.
 """
 from __future__ import annotations
 
