@@ -22,8 +22,12 @@ def layer_weights(runner, i):
     return w
 
 
-def verify_step(runner, desc, batch, capacity_of, proposals, slots, positions):
-    """Returns dict(final_hidden, logits, predictions, k_new[l], v_new[l], caches_after_write)."""
+def verify_step(runner, desc, batch, capacity_of, proposals, slots, positions, head_rows=None):
+    """Returns dict(final_hidden, logits, predictions, k_new[l], v_new[l], attention[l]).
+
+    With `head_rows` (flat row indices r * T + t), the lm_head and argmax run on those rows only
+    and `logits` / `predictions` hold them in that order (the full-vocabulary head over every row
+    of a 1008-row step is too slow for the CPU oracle)."""
     proposals = np.asarray(proposals, np.int32)
     R, T = proposals.shape
     H = desc.hidden
@@ -69,7 +73,8 @@ def verify_step(runner, desc, batch, capacity_of, proposals, slots, positions):
         nxt = weights[li + 1]["input_norm"] if li + 1 < len(desc.layers) else final_norm
         x, _ = oracle.rms_norm(hidden, nxt, eps=desc.rms_norm_epsilon)
     out["final_hidden"] = x
-    pred, logits = oracle.fp8_lm_head_argmax(x, emb_q, emb_s)
+    pred, logits = oracle.fp8_lm_head_argmax(x if head_rows is None else x[np.asarray(head_rows)],
+                                             emb_q, emb_s)
     out["predictions"] = pred
     out["logits"] = logits
     return out

@@ -311,3 +311,56 @@ def test_config5_draft_step_full_dimensions(full_model):
     err = np.abs(g - e).max() / np.abs(e).max()
     say(f"  draft hidden hand-off max rel err {err:.2e}")
     assert err <= 2e-2
+
+
+def test_config5_prefill_step_full_dimensions(full_model):
+    """One batched prefill step at the benchmark's prefill shape (prefill_slots_chunks,
+    batch_model_runner.h:40-43: 24 slots x 42 rows = 1008 rows in one forced step, the GEMMs'
+    four-tile layout) over resident contexts of U[1024, 8100] tokens that complete in this step:
+    K/V rows of both layers against tests/runner_oracle.verify_step, each slot's returned token
+    (its last row's argmax) a near-tie of the oracle's, positions advanced, and the hidden
+    hand-off equal to the step's last row of each slot."""
+    desc, runner, _ = full_model
+    rng = np.random.default_rng(59)
+    rows = 42
+    positions = rng.integers(1024, MAX_CONTEXT - rows - 8, SLOTS).astype(np.int32)
+    for slot, p in enumerate(positions):
+        runner.set_slot_position(slot, int(p))
+    slots = rng.permutation(SLOTS).astype(np.int32)
+    positions = positions[slots]
+    prompts = [rng.integers(0, VOCAB, int(p) + rows).astype(np.int32) for p in positions]
+    chunk = np.stack([pr[p:] for pr, p in zip(prompts, positions)])
+    last_rows = np.arange(SLOTS) * rows + rows - 1
+    say("case: config-5 prefill step oracle (CPU, 1008 rows)")
+    expect = verify_step(runner, desc, SLOTS, capacity_of(desc), chunk, slots, positions,
+                         head_rows=last_rows)
+    say("case: config-5 prefill_slots_chunks (24 slots x 42 rows)")
+    tokens = runner.prefill_slots_chunks(slots.tolist(), [pr.tolist() for pr in prompts], rows)
+    pred = np.array(runner.last_predictions, np.int32)
+    assert len(pred) == SLOTS * rows
+    assert tokens == pred[last_rows].tolist()
+    logits = oracle.bf16_to_f32(expect["logits"]).astype(np.float64)
+    gap = logits.max(1) - logits[np.arange(SLOTS), pred[last_rows]]
+    mism = int(np.sum(pred[last_rows] != expect["predictions"]))
+    say(f"  prefill argmax mismatches vs oracle {mism}/{SLOTS}, max gap {gap.max():.3e}")
+    assert np.all(gap <= 2 * 2 ** -7 * np.abs(logits).max(1))
+    for li in range(len(desc.layers)):
+        C = capacity_of(desc)(li)
+        for kind in ("k", "v"):
+            cache = runner.read(f"cache.{li}.{kind}", np.uint16).reshape(SLOTS, 16, C, 128)
+            got = oracle.bf16_to_f32(np.stack([cache[s][:, (p + np.arange(rows)) % C].transpose(1, 0, 2)
+                                               for s, p in zip(slots, positions)]))
+            want = oracle.bf16_to_f32(expect[f"{kind}_new"][li])
+            err = np.abs(got - want).max() / np.abs(want).max()
+            rms = np.sqrt(np.mean((got - want) ** 2)) / np.abs(want).max()
+            say(f"  layer {li} {kind} rows max rel err {err:.2e}, rms {rms:.2e}")
+            assert err <= 3e-2 and rms <= 1e-2, (li, kind)
+    final_hidden = runner.read("final_hidden", np.uint16)[: SLOTS * rows * H].reshape(SLOTS * rows, H)
+    efh = oracle.bf16_to_f32(expect["final_hidden"]).astype(np.float64)
+    err = np.abs(oracle.bf16_to_f32(final_hidden).astype(np.float64) - efh).max() / np.abs(efh).max()
+    say(f"  final hidden max rel err {err:.2e}")
+    assert err <= 3e-2
+    hidden_after = runner.read("target_hidden", np.uint16).reshape(SLOTS, H)
+    for r, slot in enumerate(slots):
+        assert np.array_equal(hidden_after[slot], final_hidden[last_rows[r]])
+        assert runner.slot_position(int(slot)) == positions[r] + rows
