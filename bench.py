@@ -17,7 +17,8 @@ dominant kernel by total time, the global verify attention, after the timed step
 layer's attention over its own cache runs back to back on the runner's stream between one pair of
 HIP events (two passes), so the per-launch figure is kernel time as a profiler sees it, not
 event-marker overhead. `roofline_gate_up` (the largest GEMM), `roofline_attention_sliding` and
-`gemms` (every per-layer FP8 GEMM) are timed the same way.
+`gemms` (every per-layer FP8 GEMM) are timed the same way; each `gemms` entry also carries the
+vendor library's time (torch._scaled_mm, i.e. hipBLASLt, with cold weights) at the same shape.
 """
 from __future__ import annotations
 
@@ -136,12 +137,42 @@ def gemm_plan(n, k, gate_up):
     return f.value, w.value, sp.value
 
 
-def gemm_table(runner, desc, rows):
+def library_gemm_us(m, n, k, cycle_bytes=1200 << 20):
+    """The vendor library's time for the same fp8 GEMM shape, as a comparison: torch._scaled_mm
+    (hipBLASLt on ROCm) with per-tensor scales and a bf16 output, cycling through enough weight
+    copies (> the 256 MB memory-side cache) that every launch reads its weights from HBM, as each
+    layer's GEMM does in the step. It has no split-K partials and no GELU epilogue."""
+    import torch
+    copies = max(2, -(-cycle_bytes // (n * k)))
+    gen = torch.Generator(device="cuda").manual_seed(11)
+    a = (torch.randn(m, k, device="cuda", generator=gen) * 0.5).to(torch.float8_e4m3fn)
+    ws = [(torch.randn(n, k, device="cuda", generator=gen) * 0.5).to(torch.float8_e4m3fn).t()
+          for _ in range(copies)]
+    one = torch.ones((), device="cuda")
+    run = lambda w: torch._scaled_mm(a, w, scale_a=one, scale_b=one, out_dtype=torch.bfloat16)
+    for w in ws:
+        run(w)
+    reps = max(20, 2 * copies)
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for i in range(reps):
+        run(ws[i % copies])
+    stop.record()
+    torch.cuda.synchronize()
+    us = start.elapsed_time(stop) * 1e3 / reps
+    del ws
+    torch.cuda.empty_cache()
+    return us
+
+
+def gemm_table(runner, desc, rows, library=True):
     """Every per-layer fp8 GEMM of the verify step timed back to back over all 60 layers' weights
     (stream_gemm_probe, two passes): HBM fraction of 8 TB/s over the algorithmic bytes (e4m3
     weights + e4m3 activations + outputs: fp32 split-K partials or the bf16 GELU output), raw fp8
     MFMA use (2*M*N*K flops per launch / 5 PFLOP/s), and the attainable MFMA use at that
-    arithmetic intensity (min(1, AI * 8 TB/s / 5 PFLOP/s))."""
+    arithmetic intensity (min(1, AI * 8 TB/s / 5 PFLOP/s)). With `library`, each entry also
+    carries the vendor library's time for the same shape (library_gemm_us) and the speedup over it."""
     H, I = desc.hidden, desc.intermediate
     g = next(l for l in desc.layers if not l.sliding)
     qkv_n = (g.query_heads + 2 * g.kv_heads) * g.head_dimension
@@ -163,7 +194,19 @@ def gemm_table(runner, desc, rows):
             "bytes_per_launch": nbytes, "GB_s": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
             "mfma_util": round(util, 4), "mfma_attainable": round(attainable, 4),
             "frac_of_attainable": round(util / attainable, 4)}
+    if library:
+        add_library_times(out, rows)
     return out
+
+
+def add_library_times(table, rows):
+    """Adds the vendor library's time at each gemm_table entry's shape. Run it after every timing
+    of this library's kernels: the kernels measured right after a burst of library GEMMs run
+    slower (gate/up 45 -> 55 us, global attention 281 -> 296 us)."""
+    for entry in table.values():
+        lib_us = library_gemm_us(rows, entry["n"], entry["k"])
+        entry["hipblaslt_us"] = round(lib_us, 2)
+        entry["speedup_vs_hipblaslt"] = round(lib_us / entry["avg_launch_us"], 3)
 
 
 def cpu_baseline(mean_accepted_per_step):
@@ -311,11 +354,11 @@ def attention_shapes(reps: int = 10) -> dict:
     return {"metric": "attention kernel time per launch (cold HBM)", "unit": "us", "cases": out}
 
 
-def prefill_throughput(tokens: int, seed: int) -> dict:
+def prefill_throughput(tokens: int, seed: int, library: bool = True) -> dict:
     """Prefill of the config-5 model from empty slots: prefill_slots_chunks over all 24 slots
     (forced steps sharing the 1024-row step budget: 42 rows per slot), then prefill_slot on one
     slot (forced steps of up to 1024 rows, the sliding ring). Prompt tokens made resident per
-    second."""
+    second; `gemms` times the per-layer GEMMs at the 1008-row step shape (gemm_table)."""
     from carat_amd import lib
     from carat_amd.runner import BatchModelRunner, ModelDesc
     rng = np.random.default_rng(seed)
@@ -349,12 +392,18 @@ def prefill_throughput(tokens: int, seed: int) -> dict:
     runner.prefill_slot(0, prompts[0], tokens)
     lib().carat_hip_synchronize()
     single = time.perf_counter() - t0
+    # the per-layer GEMMs at the 1008-row step shape (one more 42-row-per-slot step sets it)
+    for s in slots:
+        runner.reset_slot(s)
+    runner.prefill_slots_chunks(slots, prompts, per_step)
+    gemms = gemm_table(runner, desc, SLOTS * per_step, library=library)
     return {"metric": "prefill tokens/s (24 slots, config-5 model, forced steps of 42 rows per slot)",
             "value": round(SLOTS * tokens / seconds, 1), "unit": "tokens/s",
             "prompt_tokens": tokens, "slots": SLOTS, "seconds": round(seconds, 3),
             "calls": calls, "chunk_tokens": quantum,
             "single_slot": {"value": round(tokens / single, 1), "unit": "tokens/s",
-                            "seconds": round(single, 4), "steps": (tokens + 1023) // 1024}}
+                            "seconds": round(single, 4), "steps": (tokens + 1023) // 1024},
+            "gemms": gemms}
 
 
 def acceptance_config1(seed: int, reps: int = 20) -> dict:
@@ -417,6 +466,8 @@ def main() -> int:
     ap.add_argument("--seed", type=int, default=1)
     ap.add_argument("--graphs", action="store_true", help="replay the verify step as a HIP graph")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-library-compare", action="store_true",
+                    help="skip timing the vendor library (hipBLASLt) at the per-layer GEMM shapes")
     ap.add_argument("--breakdown", action="store_true", help="probe every kernel kind (stderr)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run one 256 MiB device-to-device copy (the reference kernel for "
@@ -440,6 +491,11 @@ def main() -> int:
               f"--gpus {args.gpus}); the verify step would shard by slot, one rank per GPU",
               file=sys.stderr)
         return 2
+    if not args.no_library_compare:
+        # torch's HIP runtime must be initialised before this library's first HIP call, or
+        # torch finds no device later (the library-comparison timings use torch)
+        import torch
+        torch.cuda.init()
     if args.attention_shapes:
         print(json.dumps(attention_shapes()))
         return 0
@@ -447,7 +503,7 @@ def main() -> int:
         print(json.dumps(acceptance_config1(args.seed)))
         return 0
     if args.prefill:
-        print(json.dumps(prefill_throughput(args.prefill, args.seed)))
+        print(json.dumps(prefill_throughput(args.prefill, args.seed, not args.no_library_compare)))
         return 0
     from carat_amd import lib
     from carat_amd.runner import BatchModelRunner, ModelDesc
@@ -502,7 +558,7 @@ def main() -> int:
             f"wall={1e3 * seconds:.2f}ms draft={runner.timing()[1]:.2f}ms "
             f"verify={runner.timing()[0]:.2f}ms{' (timed)' if timed else ''}")
     avg_launch_ms, probe_launches = runner.stream_gemm_probe("gate_up_gemm", passes=2)
-    gemms = gemm_table(runner, desc, SLOTS * DEPTH)
+    gemms = gemm_table(runner, desc, SLOTS * DEPTH, library=False)
     # the verify attention kernels, the way the gate/up GEMM is timed: after one planted dry
     # verify, every global (sliding) layer's attention over its own cache back to back, two
     # passes, between one pair of HIP events on the runner's stream
@@ -615,6 +671,8 @@ def main() -> int:
         "bytes_per_launch": sliding_bytes,
         "timing": "every sliding layer's attention back to back, two passes, one pair of HIP events",
     }
+    if not args.no_library_compare:
+        add_library_times(gemms, SLOTS * DEPTH)  # last: it slows the kernels timed after it
     if breakdown:
         result["kernels_ms_per_verify"] = breakdown
     if not args.no_cpu_baseline and not args.native:
