@@ -406,7 +406,7 @@ def prefill_throughput(tokens: int, seed: int, library: bool = True) -> dict:
             "gemms": gemms}
 
 
-def acceptance_config1(seed: int, reps: int = 20) -> dict:
+def acceptance_config1(seed: int, reps: int = 20, cpu_baseline: bool = True) -> dict:
     """Config 1 on the GPU: argmax over 24 x 5 x 262144 fp32 logits N(0,1) + greedy acceptance
     with drafts planted as the row argmax at p = 0.7 per position (carat_hip_argmax_accept, the
     op-level entry point). `reps` back-to-back calls between two HIP events on torch's stream."""
@@ -452,10 +452,48 @@ def acceptance_config1(seed: int, reps: int = 20) -> dict:
     torch.cuda.synchronize()
     us = start.elapsed_time(stop) * 1e3 / reps
     nbytes = R * T * V * 4
-    return {"metric": "config 1 argmax + greedy acceptance (24 x 5 x 262144 fp32 logits)",
-            "us": round(us, 2), "unit": "us per call", "bytes": nbytes,
-            "GB_s": round(nbytes / us / 1e3, 1), "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4),
-            "mean_accepted": round(float(acc.float().mean()), 3)}
+    out = {"metric": "config 1 argmax + greedy acceptance (24 x 5 x 262144 fp32 logits)",
+           "us": round(us, 2), "unit": "us per call", "bytes": nbytes,
+           "GB_s": round(nbytes / us / 1e3, 1), "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4),
+           "mean_accepted": round(float(acc.float().mean()), 3)}
+    if cpu_baseline:
+        out["cpu_baseline"] = acceptance_cpu_baseline(
+            logits.cpu().numpy(), proposals, first,
+            (pred.cpu().numpy(), acc.cpu().numpy(), nxt.cpu().numpy()))
+    return out
+
+
+def acceptance_cpu_baseline(logits, proposals, first, gpu, seconds=3.0):
+    """Config 1 on the host: the oracle's OpenMP row argmax over the same fp32 logits (ranked as
+    bf16), its greedy acceptance (batch_model_runner.cu:1738-1759), and per slot the reference's
+    own acceptance_cap and commit_speculation (speculation.cpp, compiled into oracle/_ref when
+    the reference tree was present at build time; the oracle's restatement otherwise), repeated
+    for about `seconds`. Also reports whether the host results equal the GPU's."""
+    from oracle import oracle
+    R, T = proposals.shape
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    use_ref = oracle.ref() is not None
+    cap = oracle.ref_acceptance_cap if use_ref else oracle.acceptance_cap
+    commit = oracle.ref_commit_speculation if use_ref else oracle.commit_speculation
+    calls = 0
+    t0 = time.perf_counter()
+    while True:
+        pred = oracle.argmax_f32_rows_as_bf16(logits)
+        caps = np.array([cap(T, 1 << 20, proposals[r], []) for r in range(R)], np.int32)
+        acc, nxt = oracle.greedy_accept(proposals, first, pred.reshape(R, T), caps)
+        for r in range(R):
+            commit(int(first[r]), proposals[r, 1:max(int(acc[r]), 1)].tolist(), int(nxt[r]), [])
+        calls += 1
+        elapsed = time.perf_counter() - t0
+        if elapsed >= seconds:
+            break
+    matches = (np.array_equal(pred, gpu[0]) and np.array_equal(acc, gpu[1]) and
+               np.array_equal(nxt, gpu[2]))
+    return {"value": round(1e6 * elapsed / calls, 1), "unit": "us per call", "cores": threads,
+            "kind": "reference" if use_ref else "port", "calls": calls, "matches_gpu": bool(matches),
+            "sample": "the whole config-1 workload per call: OpenMP argmax over 120 x 262144 fp32, "
+                      "greedy acceptance, 24 acceptance_cap + commit_speculation calls "
+                      f"({'reference speculation.cpp' if use_ref else 'restated speculation'})"}
 
 
 def main() -> int:
@@ -500,7 +538,7 @@ def main() -> int:
         print(json.dumps(attention_shapes()))
         return 0
     if args.acceptance:
-        print(json.dumps(acceptance_config1(args.seed)))
+        print(json.dumps(acceptance_config1(args.seed, cpu_baseline=not args.no_cpu_baseline)))
         return 0
     if args.prefill:
         print(json.dumps(prefill_throughput(args.prefill, args.seed, not args.no_library_compare)))
