@@ -8,7 +8,9 @@
 - Config 5: a verify step of a two-layer (one sliding, one global) model at full Gemma-4-31B
   benchmark dimensions (hidden 5376, intermediate 21504, vocabulary 262144, 32/16 heads x 128,
   window 1024) with 24 slots at contexts U[1024, 8187] against tests/runner_oracle.verify_step,
-  and one draft step of the full-size assistant against tests/runner_oracle.draft_steps.
+  and one draft step of the full-size assistant against tests/runner_oracle.draft_steps; one
+  1008-row batched prefill step; a verify step at Gemma-4 31B's own attention geometry
+  (sliding D 256, global D 512 with K = V).
 
 Bars: acceptance, bonus tokens, cache commit and hidden hand-off bit-exact given the GPU's own
 predictions; K/V rows and activations within 3e-2 of the row maximum; every argmax mismatch
@@ -206,8 +208,9 @@ def full_verify_case(runner, desc, slots, positions, first, depth, caps, rng, ta
     assert mism <= M // 10
     # this step's K/V rows and the final hidden rows
     for li, spec in enumerate(desc.layers):
+        kv_width = spec.kv_heads * spec.head_dimension
         for kind in ("k", "v"):
-            got = oracle.bf16_to_f32(runner.read(f"new.{li}.{kind}", np.uint16)[: M * 16 * 128])
+            got = oracle.bf16_to_f32(runner.read(f"new.{li}.{kind}", np.uint16)[: M * kv_width])
             want = oracle.bf16_to_f32(expect[f"{kind}_new"][li]).reshape(-1)
             err = np.abs(got - want).max() / np.abs(want).max()
             say(f"  layer {li} {kind} rows max rel err {err:.2e}")
@@ -220,10 +223,11 @@ def full_verify_case(runner, desc, slots, positions, first, depth, caps, rng, ta
     # commit: exact cache bytes, hidden hand-off and positions
     for li in (li_s, li_g):
         C = capacity_of(desc)(li)
-        k_exp = before[li][0].reshape(SLOTS, 16, C, 128)
-        v_exp = before[li][1].reshape(SLOTS, 16, C, 128)
-        k_new = runner.read(f"new.{li}.k", np.uint16)[: M * 2048].reshape(SLOTS, T, 16, 128)
-        v_new = runner.read(f"new.{li}.v", np.uint16)[: M * 2048].reshape(SLOTS, T, 16, 128)
+        hkv, D = desc.layers[li].kv_heads, desc.layers[li].head_dimension
+        k_exp = before[li][0].reshape(SLOTS, hkv, C, D)
+        v_exp = before[li][1].reshape(SLOTS, hkv, C, D)
+        k_new = runner.read(f"new.{li}.k", np.uint16)[: M * hkv * D].reshape(SLOTS, T, hkv, D)
+        v_new = runner.read(f"new.{li}.v", np.uint16)[: M * hkv * D].reshape(SLOTS, T, hkv, D)
         kept = res.accepted_tokens if desc.layers[li].sliding else [T] * SLOTS
         oracle.commit_kv(k_exp, v_exp, k_new, v_new, slots, positions, kept, C)
         assert np.array_equal(runner.read(f"cache.{li}.k", np.uint16), k_exp.reshape(-1)), li
@@ -235,6 +239,38 @@ def full_verify_case(runner, desc, slots, positions, first, depth, caps, rng, ta
         want = final_hidden[r * T + a - 1] if a > 0 else hidden_before[slot]
         assert np.array_equal(hidden_after[slot], want)
         assert runner.slot_position(int(slot)) == positions[r] + a
+
+
+@pytest.fixture(scope="module")
+def native_model(torch_cuda):
+    """Gemma-4 31B's own attention geometry (gemma4_config.cpp:174-203) at full hidden,
+    intermediate and vocabulary: a sliding layer with 32/16 heads x 256 and a global layer with
+    32/4 heads x 512 and K = V; no assistant."""
+    desc = ModelDesc(hidden=H, intermediate=INTER, vocabulary=VOCAB, sliding_window=1024,
+                     layers=[LayerSpec(True, 32, 16, 256),
+                             LayerSpec(False, 32, 4, 512, key_equals_value=True)],
+                     assistant=False, seed=6, weight_std=0.02)
+    say("case: native-geometry two-layer runner create (24 slots, context 8192)")
+    runner = BatchModelRunner(desc, SLOTS, MAX_CONTEXT)
+    rng = np.random.default_rng(65)
+    positions = rng.integers(1024, MAX_CONTEXT - T + 1, SLOTS).astype(np.int32)
+    runner.seed_random_cache(int(positions.max()), seed=8, stddev=1 / math.sqrt(256))
+    for slot, p in enumerate(positions):
+        runner.set_slot_position(slot, int(p))
+    yield desc, runner, positions
+    runner.close()
+
+
+def test_native_geometry_verify_step_full_dimensions(native_model):
+    """One verify step at the native geometry: qkv 5376 -> 16384 (sliding) and 18432 (global,
+    K = V), o 8192 / 16384 -> 5376, the D 256 sliding and D 512 global verify attention kernels
+    (40 query rows per kv head), against the oracle composition with the same bars as config 5."""
+    desc, runner, positions_by_slot = native_model
+    rng = np.random.default_rng(66)
+    slots = rng.permutation(SLOTS).astype(np.int32)
+    positions = positions_by_slot[slots]
+    first = rng.integers(0, VOCAB, SLOTS).astype(np.int32)
+    full_verify_case(runner, desc, slots, positions, first, T, None, rng, "native")
 
 
 def test_config5_verify_step_full_dimensions(full_model):
