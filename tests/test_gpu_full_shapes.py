@@ -245,11 +245,11 @@ def full_verify_case(runner, desc, slots, positions, first, depth, caps, rng, ta
 def native_model(torch_cuda):
     """Gemma-4 31B's own attention geometry (gemma4_config.cpp:174-203) at full hidden,
     intermediate and vocabulary: a sliding layer with 32/16 heads x 256 and a global layer with
-    32/4 heads x 512 and K = V; no assistant."""
+    32/4 heads x 512 and K = V, and the full-size assistant over those caches."""
     desc = ModelDesc(hidden=H, intermediate=INTER, vocabulary=VOCAB, sliding_window=1024,
                      layers=[LayerSpec(True, 32, 16, 256),
                              LayerSpec(False, 32, 4, 512, key_equals_value=True)],
-                     assistant=False, seed=6, weight_std=0.02)
+                     assistant=True, seed=6, weight_std=0.02)
     say("case: native-geometry two-layer runner create (24 slots, context 8192)")
     runner = BatchModelRunner(desc, SLOTS, MAX_CONTEXT)
     rng = np.random.default_rng(65)
@@ -271,6 +271,32 @@ def test_native_geometry_verify_step_full_dimensions(native_model):
     positions = positions_by_slot[slots]
     first = rng.integers(0, VOCAB, SLOTS).astype(np.int32)
     full_verify_case(runner, desc, slots, positions, first, T, None, rng, "native")
+
+
+def test_native_geometry_draft_step_full_dimensions(native_model):
+    """A forced step and one free step of the assistant whose attention reads the native caches
+    (decode attention at D 256 over the sliding ring and D 512 over the K = V global cache)."""
+    desc, runner, _ = native_model
+    rng = np.random.default_rng(67)
+    slots = rng.permutation(SLOTS).astype(np.int32).tolist()
+    last = rng.integers(0, VOCAB, SLOTS).astype(np.int32).tolist()
+    forced = rng.integers(0, VOCAB, SLOTS).astype(np.int32).tolist()
+    say("case: native-geometry draft (depth 2, forced first token)")
+    got = np.array(runner.draft_four(last, slots, forced, 2), np.int32)
+    assert got[:, 0].tolist() == forced
+    exp = draft_steps(runner, desc, SLOTS, capacity_of(desc), last, slots, forced, 2, feed=got)
+    logits = oracle.bf16_to_f32(exp["logits"][1]).astype(np.float64)
+    gap = logits.max(1) - logits[np.arange(SLOTS), got[:, 1]]
+    mism = int(np.sum(got[:, 1] != exp["tokens"][:, 1]))
+    say(f"  native draft argmax mismatches vs oracle {mism}/{SLOTS}, max gap {gap.max():.3e}")
+    assert np.all(gap <= 2 * 2 ** -7 * np.abs(logits).max(1))
+    assert mism <= 2
+    hidden = runner.read("assistant.previous_hidden", np.uint16).reshape(SLOTS, H)
+    g = oracle.bf16_to_f32(hidden).astype(np.float64)
+    e = oracle.bf16_to_f32(exp["hidden"][-1]).astype(np.float64)
+    err = np.abs(g - e).max() / np.abs(e).max()
+    say(f"  native draft hidden hand-off max rel err {err:.2e}")
+    assert err <= 2e-2
 
 
 def test_config5_verify_step_full_dimensions(full_model):
