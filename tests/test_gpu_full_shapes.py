@@ -375,6 +375,45 @@ def test_config5_draft_step_full_dimensions(full_model):
     assert err <= 2e-2
 
 
+def test_config5_append_ragged_full_dimensions(full_model):
+    """append_ragged (batch_model_runner.cu:1544-1615) over all 24 slots at config-5 dimensions:
+    a depth-1 step of 24 rows, which takes the GEMMs' small-M kernels (two 16-token tiles) at the
+    runner's qkv, o, gate/up, down and lm_head shapes. Next tokens against the oracle (near-ties
+    only), this step's K/V rows, their commit at each slot's position, positions + 1."""
+    desc, runner, _ = full_model
+    rng = np.random.default_rng(60)
+    positions = rng.integers(1024, MAX_CONTEXT - 8, SLOTS).astype(np.int32)
+    for slot, p in enumerate(positions):
+        runner.set_slot_position(slot, int(p))
+    slots = rng.permutation(SLOTS).astype(np.int32)
+    positions = positions[slots]
+    tokens = rng.integers(0, VOCAB, SLOTS).astype(np.int32)
+    say("case: config-5 append_ragged oracle (CPU, 24 rows)")
+    expect = verify_step(runner, desc, SLOTS, capacity_of(desc), tokens[:, None], slots, positions)
+    say("case: config-5 append_ragged")
+    nxt = np.array(runner.append_ragged(tokens.tolist(), slots.tolist()), np.int32)
+    logits = oracle.bf16_to_f32(expect["logits"]).astype(np.float64)
+    gap = logits.max(1) - logits[np.arange(SLOTS), nxt]
+    mism = int(np.sum(nxt != expect["predictions"]))
+    say(f"  append_ragged argmax mismatches vs oracle {mism}/{SLOTS}, max gap {gap.max():.3e}")
+    assert np.all(gap <= 2 * 2 ** -7 * np.abs(logits).max(1))
+    assert mism <= 2
+    for li, spec in enumerate(desc.layers):
+        C = capacity_of(desc)(li)
+        hkv, D = spec.kv_heads, spec.head_dimension
+        for kind in ("k", "v"):
+            new = runner.read(f"new.{li}.{kind}", np.uint16)[: SLOTS * hkv * D].reshape(SLOTS, hkv, D)
+            want = oracle.bf16_to_f32(expect[f"{kind}_new"][li][:, 0])
+            err = np.abs(oracle.bf16_to_f32(new) - want).max() / np.abs(want).max()
+            say(f"  layer {li} {kind} row max rel err {err:.2e}")
+            assert err <= 3e-2, (li, kind)
+            cache = runner.read(f"cache.{li}.{kind}", np.uint16).reshape(SLOTS, hkv, C, D)
+            for r, slot in enumerate(slots):
+                assert np.array_equal(cache[slot, :, positions[r] % C], new[r]), (li, kind, r)
+    for r, slot in enumerate(slots):
+        assert runner.slot_position(int(slot)) == positions[r] + 1
+
+
 def test_config5_prefill_step_full_dimensions(full_model):
     """One batched prefill step at the benchmark's prefill shape (prefill_slots_chunks,
     batch_model_runner.h:40-43: 24 slots x 42 rows = 1008 rows in one forced step, the GEMMs'
