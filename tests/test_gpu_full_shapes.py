@@ -465,3 +465,41 @@ def test_config5_prefill_step_full_dimensions(full_model):
     for r, slot in enumerate(slots):
         assert np.array_equal(hidden_after[slot], final_hidden[last_rows[r]])
         assert runner.slot_position(int(slot)) == positions[r] + rows
+
+
+def test_config5_deep_prefill_step_full_dimensions(full_model):
+    """One slot's 1024-row prefill step (prefill_slot_chunk, batch_model_runner.h:38-39) over a
+    resident context of 3000 tokens at config-5 dimensions: the whole sliding ring is rewritten
+    in one step, the attention runs its 32-row query tiles over the causal triangle and the
+    sliding band, and the GEMMs run eight token blocks per weight block for one request. K/V rows
+    of both layers against the oracle, the returned token a near-tie of the oracle's, the position
+    advanced."""
+    desc, runner, _ = full_model
+    rng = np.random.default_rng(61)
+    rows, slot, p = 1024, 7, 3000
+    runner.set_slot_position(slot, p)
+    prompt = rng.integers(0, VOCAB, p + rows).astype(np.int32)
+    say("case: config-5 deep prefill step oracle (CPU, 1024 rows)")
+    expect = verify_step(runner, desc, SLOTS, capacity_of(desc), prompt[None, p:], [slot],
+                         np.array([p], np.int32), head_rows=[rows - 1])
+    say("case: config-5 prefill_slot_chunk (one slot, 1024 rows)")
+    token = runner.prefill_slot_chunk(slot, prompt.tolist(), rows)
+    pred = np.array(runner.last_predictions, np.int32)
+    assert token == int(pred[rows - 1])
+    logits = oracle.bf16_to_f32(expect["logits"]).astype(np.float64)
+    gap = logits.max(1) - logits[0, token]
+    say(f"  deep prefill token {token} vs oracle {int(expect['predictions'][0])}, gap {gap[0]:.3e}")
+    assert np.all(gap <= 2 * 2 ** -7 * np.abs(logits).max(1))
+    for li, spec in enumerate(desc.layers):
+        C = capacity_of(desc)(li)
+        hkv, D = spec.kv_heads, spec.head_dimension
+        for kind in ("k", "v"):
+            cache = runner.read(f"cache.{li}.{kind}", np.uint16).reshape(SLOTS, hkv, C, D)
+            got = oracle.bf16_to_f32(cache[slot][:, (p + np.arange(rows)) % C].transpose(1, 0, 2))
+            want = oracle.bf16_to_f32(expect[f"{kind}_new"][li][0])
+            err = np.abs(got - want).max() / np.abs(want).max()
+            rms = np.sqrt(np.mean((got - want) ** 2)) / np.abs(want).max()
+            say(f"  layer {li} {kind} rows max rel err {err:.2e}, rms {rms:.2e}")
+            assert err <= 3e-2 and rms <= 1e-2, (li, kind)
+    assert runner.slot_position(slot) == p + rows
+
