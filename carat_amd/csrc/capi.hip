@@ -464,11 +464,15 @@ int carat_hip_bench_speculative_cycle(carat_hip_runner *runner, int requests, in
                                                planted + static_cast<size_t>(i + 1) * depth);
     hip_check(hipDeviceSynchronize(), "synchronise before the speculative cycle");
     const auto start = std::chrono::steady_clock::now();
-    // native_runtime_main.cpp:583-678: draft, caps from the draft, verify, commit
+    // native_runtime_main.cpp:583-678: draft, caps from the proposals, verify, commit. The
+    // proposals verified are the planted ones (they replace the drafts), so the caps are taken
+    // from them, as the reference takes them from the drafts it verifies.
     const auto drafts = r.draft_four(last, slot_list, first, depth);
+    if (drafts.size() != static_cast<size_t>(requests))
+      throw std::runtime_error("draft returned the wrong number of rows");
     std::vector<int> caps(static_cast<size_t>(requests));
     for (int i = 0; i < requests; ++i)
-      caps[static_cast<size_t>(i)] = acceptance_cap(depth, remaining, drafts[static_cast<size_t>(i)], stops);
+      caps[static_cast<size_t>(i)] = acceptance_cap(depth, remaining, proposals[static_cast<size_t>(i)], stops);
     const GreedyVerificationResult result = r.verify_greedy_proposals(proposals, first, slot_list, caps);
     for (int i = 0; i < requests; ++i) {
       const int a = result.accepted_tokens[static_cast<size_t>(i)];

@@ -270,9 +270,12 @@ struct BatchModelRunner::Implementation {
   std::pair<hipEvent_t, hipEvent_t> probe(int kind) {
     if (kind == probe_none || kind != probe_kind) return {nullptr, nullptr};
     if (probe_used == probe_pool.size()) {
-      hipEvent_t a, b;
+      hipEvent_t a = nullptr, b = nullptr;
       hip_check(hipEventCreate(&a), "create probe event");
-      hip_check(hipEventCreate(&b), "create probe event");
+      if (hipEventCreate(&b) != hipSuccess) {
+        (void)hipEventDestroy(a);
+        throw std::runtime_error("create probe event failed");
+      }
       probe_pool.emplace_back(a, b);
     }
     return probe_pool[probe_used++];
@@ -806,9 +809,16 @@ struct BatchModelRunner::Implementation {
       }
     };
     if (!attention) launch(0, false);  // prepares the activation operand once
-    hipEvent_t start, stop;
-    hip_check(hipEventCreate(&start), "create probe event");
-    hip_check(hipEventCreate(&stop), "create probe event");
+    struct Events {  // destroyed on every exit, errors included
+      hipEvent_t start = nullptr, stop = nullptr;
+      ~Events() {
+        if (start != nullptr) (void)hipEventDestroy(start);
+        if (stop != nullptr) (void)hipEventDestroy(stop);
+      }
+    } ev;
+    hip_check(hipEventCreate(&ev.start), "create probe event");
+    hip_check(hipEventCreate(&ev.stop), "create probe event");
+    hipEvent_t start = ev.start, stop = ev.stop;
     hip_check(hipEventRecord(start, stream), "record probe");
     for (int pass = 0; pass < passes; ++pass)
       for (size_t li = 0; li < layers.size(); ++li) launch(li, true);
@@ -816,8 +826,6 @@ struct BatchModelRunner::Implementation {
     hip_check(hipEventSynchronize(stop), "probe sync");
     float ms = 0.0f;
     hip_check(hipEventElapsedTime(&ms, start, stop), "probe time");
-    hip_check(hipEventDestroy(start), "destroy probe event");
-    hip_check(hipEventDestroy(stop), "destroy probe event");
     size_t per_pass = layers.size();
     if (attention) {
       per_pass = 0;

@@ -207,8 +207,9 @@ int carat_hip_runner_set_fused_quantization(carat_hip_runner *runner, int enable
 int carat_hip_runner_timing(carat_hip_runner *runner, float *verify_ms, float *draft_ms);
 /* Benchmark helper, no counterpart in the reference: one speculative cycle of the reference's
  * scheduler (native_runtime_main.cpp:583-678) in C++ -- draft_four(last, slots, forced, depth),
- * acceptance_cap per request over the drafts, verify_greedy_proposals over `planted` [requests]
- * [depth] (the benchmark's proposals, row 0 = forced) with those caps, commit_speculation per
+ * acceptance_cap per request over `planted` [requests][depth] (the benchmark's proposals, row 0
+ * = forced, which replace the drafts), verify_greedy_proposals over them with those caps,
+ * commit_speculation per
  * request -- timed on the host clock from a synchronised device (*seconds_out). Writes the
  * accepted counts, the next forced token and the last resident token of every request. */
 int carat_hip_bench_speculative_cycle(carat_hip_runner *runner, int requests, int depth,
