@@ -377,8 +377,11 @@ def test_prefill_steps_match_oracle_and_one_call(model):
         else:
             logits = oracle.bf16_to_f32(expect["logits"]).astype(np.float64).reshape(T, -1)
             gap = logits.max(1) - logits[np.arange(T), pred]
-            assert np.mean(pred == expect["predictions"]) >= 0.85
-            assert np.all(gap <= 0.05 * logits.std())
+            mism = int(np.sum(pred != expect["predictions"]))
+            say(f"  prefill argmax mismatches vs oracle {mism}/{T}, max gap {gap.max():.3e}")
+            # a mismatch is a near-tie: within 2 bf16 ulps of the row maximum
+            assert np.all(gap <= 2 * 2 ** -7 * np.abs(logits).max(1))
+            assert mism <= max(1, T // 10)
         for li, spec in enumerate(desc.layers):
             C = capacity_of(desc)(li)
             kc = runner.read(f"cache.{li}.k", np.uint16).reshape(BATCH, 2, C, 128)
