@@ -111,8 +111,11 @@ def test_verify_step_over_checkpoint_weights(loaded):
     pred = np.array(runner.last_predictions, np.int32)
     logits = oracle.bf16_to_f32(expect["logits"]).astype(np.float64).reshape(4 * T, -1)
     gap = logits.max(1) - logits[np.arange(4 * T), pred]
-    assert np.mean(pred == expect["predictions"]) >= 0.85
-    assert np.all(gap <= 0.05 * logits.std())
+    mism = int(np.sum(pred != expect["predictions"]))
+    say(f"  argmax mismatches vs oracle {mism}/{4 * T}, max gap {gap.max():.3e}")
+    # a mismatch is a near-tie: within 2 bf16 ulps of the row maximum
+    assert np.all(gap <= 2 * 2 ** -7 * np.abs(logits).max(1))
+    assert mism <= max(1, 4 * T // 10)
     drafts = runner.draft_four(first.tolist(), slots, first.tolist(), 4)
     assert [row[0] for row in drafts] == first.tolist()
 

@@ -258,7 +258,9 @@ def test_fp8_lm_head_argmax_is_bit_exact_on_its_own_logits(dev, m, k, n):
     o32 = oracle.bf16_to_f32(o_logits).astype(np.float64)
     g32 = oracle.bf16_to_f32(logits).astype(np.float64)
     assert np.all(np.abs(g32 - o32) <= np.abs(o32) * 2 ** -7 + 1e-3 * np.abs(o32).max())
-    assert np.mean(pred == o_pred) >= 0.97
+    # against the oracle's own argmax, a mismatch is a near-tie (2 bf16 ulps of the row maximum)
+    gap = o32.max(1) - o32[np.arange(len(pred)), pred]
+    assert np.all(gap <= 2 * 2 ** -7 * np.abs(o32).max(1))
 
 
 # 256 and 8192: 4-wave blocks of two tiles per wave; 21504 (the verify shape): 3-wave blocks of

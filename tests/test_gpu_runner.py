@@ -309,7 +309,9 @@ def test_append_ragged_is_one_forced_decode_step(model):
     nxt = runner.append_ragged(tokens, slots)
     logits = oracle.bf16_to_f32(expect["logits"]).astype(np.float64).reshape(len(slots), -1)
     gap = logits.max(1) - logits[np.arange(len(slots)), nxt]
-    assert np.all(gap <= 0.05 * logits.std())
+    # a mismatch with the oracle is a near-tie: within 2 bf16 ulps of the row maximum
+    assert np.all(gap <= 2 * 2 ** -7 * np.abs(logits).max(1))
+    assert int(np.sum(np.array(nxt) != expect["predictions"])) <= 1
     for r, slot in enumerate(slots):
         assert runner.slot_position(slot) == positions[r] + 1
     assert runner.slot_position(2) == positions_by_slot[2]
@@ -514,8 +516,10 @@ def test_append_is_a_lock_step_decode(model):
     got = np.array(runner.append(tokens.tolist()), np.int32)
     logits = oracle.bf16_to_f32(expect["logits"]).astype(np.float64).reshape(BATCH, -1)
     gap = logits.max(1) - logits[np.arange(BATCH), got]
-    assert np.mean(got == expect["predictions"]) >= 0.75
-    assert np.all(gap <= 0.05 * logits.std())
+    mism = int(np.sum(got != expect["predictions"]))
+    say(f"  append argmax mismatches vs oracle {mism}/{BATCH}, max gap {gap.max():.3e}")
+    assert np.all(gap <= 2 * 2 ** -7 * np.abs(logits).max(1))  # near-ties only
+    assert mism <= 1
     assert runner.position() == 61 and all(runner.slot_position(s) == 61 for s in range(BATCH))
     with pytest.raises(CaratError, match="token batch has the wrong size"):
         runner.append(tokens[:2].tolist())
