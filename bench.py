@@ -213,7 +213,7 @@ def cpu_baseline(mean_accepted_per_step):
     """Plain OpenMP C evaluation (the oracle, a restatement of the reference's verify layer) timed
     on this host over a bounded sample: two sliding layers (averaged) and one global layer at the
     full config-5 shape, the whole lm_head with its argmax, and the argmax + greedy acceptance over
-    24x5 rows.
+    24x5 rows, and one assistant draft step (x5 for the draft's depth).
     Extrapolated to 50 sliding + 10 global layers."""
     from oracle import oracle
 
@@ -229,11 +229,14 @@ def cpu_baseline(mean_accepted_per_step):
     qn = bf((D,), 0.05)
     cos, sin = oracle.rope_table(D, False, MAX_CONTEXT)
 
+    caches = {sliding: (bf((R, hkv, 1024 if sliding else MAX_CONTEXT, D), 1 / math.sqrt(D)),
+                        bf((R, hkv, 1024 if sliding else MAX_CONTEXT, D), 1 / math.sqrt(D)))
+              for sliding in (True, False)}
+
     def layer(sliding):
         C = 1024 if sliding else MAX_CONTEXT
         positions = np.full(R, MAX_CONTEXT - 64, np.int32)
-        kc = bf((R, hkv, C, D), 1 / math.sqrt(D))
-        vc = bf((R, hkv, C, D), 1 / math.sqrt(D))
+        kc, vc = caches[sliding]
         t0 = time.perf_counter()
         n, _ = oracle.rms_norm(x, norm_w)
         qx, sx = oracle.quantize_e4m3(n)
@@ -260,6 +263,49 @@ def cpu_baseline(mean_accepted_per_step):
     t0 = time.perf_counter()
     oracle.fp8_lm_head_argmax(x, emb, 0.001)
     t_lm = time.perf_counter() - t0
+    del emb
+
+    # One assistant draft step (assistant_runner.cu:218-338, bf16 weights; the dims of
+    # ModelDesc's assistant): embedding | previous hidden -> pre-projection, three layers over the
+    # sliding cache and one over the global one, final norm, lm_head + argmax, post-projection.
+    AH, AI, AQ = 1024, 8192, 32
+    a_layers = [dict(q=bf((AQ * D, AH), 0.03), o=bf((AH, AQ * D), 0.03),
+                     gate_up=bf((2 * AI, AH), 0.03), down=bf((AH, AI), 0.03)) for _ in range(4)]
+    a_norm = bf((AH,), 0.05)
+    pre_w, post_w = bf((AH, 2 * H), 0.02), bf((H, AH), 0.03)
+    a_head = bf((262144, AH), 0.03)
+    token_table = bf((4096, H))  # a slice of the target embedding: the gather is not the cost
+    context = np.full(R, MAX_CONTEXT - 64, np.int32)
+    slot_ids = np.arange(R, dtype=np.int32)
+    previous = bf((R, H))
+
+    def draft_step():
+        t0 = time.perf_counter()
+        tokens = rng.integers(0, 4096, R).astype(np.int32)
+        h = oracle.bf16_linear(np.concatenate([oracle.embedding(token_table, tokens, math.sqrt(H)),
+                                               previous], axis=1), pre_w)
+        for li, w in enumerate(a_layers):
+            sliding = li < 3
+            kc, vc = caches[sliding]
+            n, _ = oracle.rms_norm(h, a_norm)
+            q, _, _ = oracle.qkv_post(oracle.bf16_linear(n, w["q"]), qn, qn, cos, sin, context, AQ, 0, D)
+            attn = oracle.decode_attention(q, kc, vc, slot_ids, context, hkv, 1024 if sliding else MAX_CONTEXT)
+            o = oracle.bf16_linear(attn.reshape(R, AQ * D), w["o"])
+            r1, pre_mlp, _ = oracle.rms_norm_add_and_norm(o, a_norm, h, a_norm)
+            act, _ = oracle.gelu_tanh_gate_rows(oracle.bf16_linear(pre_mlp, w["gate_up"]))
+            h = oracle.rms_norm_add_scale(oracle.bf16_linear(act, w["down"]), a_norm, r1, 0x3F80)
+        fh, _ = oracle.rms_norm(h, a_norm)
+        t_body = time.perf_counter() - t0
+        t1 = time.perf_counter()
+        oracle.argmax_bf16_rows(oracle.bf16_linear(fh, a_head))
+        t_head = time.perf_counter() - t1
+        t2 = time.perf_counter()
+        oracle.bf16_linear(fh, post_w)
+        return t_body + time.perf_counter() - t2, t_head
+
+    t_draft_body, t_draft_head = draft_step()
+    # depth 5: five steps, the first one forced (no lm_head)
+    t_draft = DEPTH * t_draft_body + (DEPTH - 1) * t_draft_head
     logits = rng.standard_normal((M, 262144), dtype=np.float32)
     t0 = time.perf_counter()
     pred = oracle.argmax_f32_rows_as_bf16(logits).reshape(R, T)
@@ -269,7 +315,7 @@ def cpu_baseline(mean_accepted_per_step):
             oracle.ref_acceptance_cap(DEPTH, 100, pred[r].tolist(), [1])
             oracle.ref_commit_speculation(int(pred[r, 0]), pred[r, 1:3].tolist(), int(pred[r, 3]), [1])
     t_accept = time.perf_counter() - t0
-    step = 50 * t_sliding + 10 * t_global + t_lm + t_accept
+    step = 50 * t_sliding + 10 * t_global + t_lm + t_accept + t_draft
     return {
         "value": round(mean_accepted_per_step / step, 3),
         "unit": "accepted tok/s",
@@ -277,9 +323,10 @@ def cpu_baseline(mean_accepted_per_step):
         "kind": "port",
         "sample": (f"2 sliding + 1 global verify layer at config-5 shape ({t_sliding:.2f}s each, "
                    f"{t_global:.2f}s), the whole 262144-row lm_head with argmax ({t_lm:.2f}s), "
-                   f"argmax+acceptance over 24x5x262144 ({t_accept:.2f}s); extrapolated to "
-                   f"50+10 layers = {step:.1f}s/step at {mean_accepted_per_step:.1f} accepted "
-                   "tokens/step"),
+                   f"argmax+acceptance over 24x5x262144 ({t_accept:.2f}s), one assistant draft "
+                   f"step ({t_draft_body:.2f}s + lm_head {t_draft_head:.2f}s, x5 with 4 heads -> "
+                   f"{t_draft:.2f}s); extrapolated to 50+10 layers = {step:.1f}s/step at "
+                   f"{mean_accepted_per_step:.1f} accepted tokens/step"),
     }
 
 
