@@ -151,14 +151,23 @@ def test_graph_replay_matches_eager(model):
     first = [p[0] for p in props]
     slots = [0, 1, 2, 3]
     say("case: eager vs graph replays")
+    names = ["final_hidden"] + [f"new.{li}.{kind}" for li in range(len(desc.layers)) for kind in ("k", "v")]
     runner.set_graphs(False)
     runner.verify_greedy_proposals(props, first, slots, [0] * 4)
     eager = list(runner.last_predictions)
+    eager_tensors = [runner.read(n, np.uint16).copy() for n in names]
     runner.set_graphs(True)
     try:
-        for _ in range(3):
+        for replay in range(4):
             runner.verify_greedy_proposals(props, first, slots, [0] * 4)
-            assert runner.last_predictions == eager
+            assert runner.last_predictions == eager, replay
+            for name, want in zip(names, eager_tensors):
+                assert np.array_equal(runner.read(name, np.uint16), want), (replay, name)
+            # eager work of the runner's own between replays: a draft (never captured) that
+            # overwrites the assistant's buffers, and a dry verify of another shape
+            if runner.has_assistant():
+                runner.draft_four(first, slots, first, 2)
+            runner.verify_greedy_proposals([p[:3] for p in props[:2]], first[:2], [3, 2], [0, 0])
     finally:
         runner.set_graphs(False)
 
