@@ -1,5 +1,5 @@
 #!/usr/bin/env python3
-"""End-to-end speculative-decoding step on one MI355X.
+"""End-to-end speculative-decoding step on one MI355X (benchmark config 5).
 
 Workload: a random-init Gemma-4-31B-shaped FP8 target (60 layers, 5 sliding(1024) : 1 global,
 hidden 5376, intermediate 21504, 32 query / 16 KV heads x 128, vocab 262144) and a random-init

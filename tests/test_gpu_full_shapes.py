@@ -1,4 +1,4 @@
-"""Parity at the graded shapes (BASELINE configs 4 and 5) on the GPU.
+"""Parity at the graded shapes (benchmark configs 4 and 5) on the GPU.
 
 - Config 4: the fp8 GEMMs at exactly the runner's dispatch (weight layout and split-K factor from
   carat_hip_gemm_plan): qkv 5376->8192, o 4096->5376, gate/up 5376->2x21504 with the GELU

@@ -67,7 +67,7 @@ def test_e4m3_conversion_exhaustive_over_bf16(dev):
 
 # ------------------------------------------------------------------ argmax + acceptance
 def planted_config1(rng, requests=24, tokens=5, vocab=262144, p=0.7):
-    """N(0,1) fp32 logits; draft d_{j+1} = argmax(row j) w.p. p (geometric
+    """Benchmark config 1: N(0,1) fp32 logits; draft d_{j+1} = argmax(row j) w.p. p (geometric
     acceptance), else a random non-argmax id. proposal[0] = forced = target_first."""
     logits = rng.standard_normal((requests * tokens, vocab), dtype=np.float32)
     arg = oracle.argmax_f32_rows_as_bf16(logits).reshape(requests, tokens)
