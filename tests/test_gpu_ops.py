@@ -3,7 +3,7 @@ the same seeded inputs.
 
 Bars: integer/index results (argmax, acceptance, e4m3 codes) are bit-exact; floating-point outputs
 carry the tolerance written in each test (attention: max |err| <= 2e-2 * max |ref|, the
-north-star bound against an fp32-accumulated reference).
+bound stated for attention outputs against an fp32-accumulated reference).
 """
 import math
 import sys
