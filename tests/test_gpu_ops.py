@@ -611,3 +611,79 @@ def test_native_gemma4_attention_shapes(dev, chunk):
     dummy = np.zeros((B, 1, 4, d), np.uint16)
     got = run_attention(torch, 2, q, kc, vc, dummy, dummy, slots, positions, C, 0, C, chunk=chunk)
     assert attention_err(got[:, 0], oracle.decode_attention(q[:, 0], kc, vc, slots, positions, 4, C)) <= 2e-2
+
+
+def random_attention_cases(seed, count):
+    """Seeded random verify / decode attention configurations: mode, heads per kv head, head
+    dimension, ring capacity and window, tokens per request, positions (0, just below and past a
+    wrap, random), request count, key chunking and, for global layers, e4m3 K/V."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(count):
+        mode = int(rng.choice([0, 1, 2]))
+        d = int(rng.choice([128, 128, 256, 512] if mode == 1 else [128, 128, 256]))
+        hkv = int(rng.choice([1, 2, 4]))
+        group = int(rng.choice([1, 2, 4, 8]))
+        requests = int(rng.integers(1, 5))
+        tokens = 1 if mode == 2 else int(rng.choice([1, 2, 5, 8, 17, 40]))
+        if mode == 0:
+            capacity = int(rng.choice([64, 256, 1024]))
+            window = int(rng.choice([capacity, max(16, capacity // 2)]))
+            tokens = min(tokens, capacity)
+            positions = rng.integers(0, 3 * capacity, requests)
+            positions[0] = int(rng.choice([0, capacity - 1, capacity, window - 1]))
+        elif mode == 1:
+            capacity = int(rng.choice([256, 1024, 2048]))
+            window = 0
+            positions = rng.integers(0, capacity - tokens + 1, requests)
+            positions[0] = int(rng.choice([0, capacity - tokens]))
+        else:
+            capacity = int(rng.choice([256, 1024]))
+            window = 0
+            positions = rng.integers(0, 2 * capacity, requests)
+        fp8 = mode == 1 and d == 128 and bool(rng.integers(0, 2))
+        chunk = int(rng.choice([0, 256]))
+        cases.append((i, mode, d, hkv, group, requests, tokens, capacity, window,
+                      positions.astype(np.int32), fp8, chunk))
+    return cases
+
+
+@pytest.mark.parametrize("seed", [101, 202])
+def test_attention_random_shapes(dev, seed):
+    """Twenty seeded random configurations per seed through the op-level entry point against the
+    oracle (max |err| <= 2e-2 * max |ref|): sliding rings with windows at and below their
+    capacity, positions at 0 and around a wrap, 1-40 tokens per request, 1-8 query heads per kv
+    head, D 128/256/512, single and split key ranges, bf16 and e4m3 K/V."""
+    torch = dev
+    for (i, mode, d, hkv, group, requests, tokens, capacity, window, positions, fp8,
+         chunk) in random_attention_cases(seed, 20):
+        hq = hkv * group
+        rng = np.random.default_rng(seed * 1000 + i)
+        say(f"case: seed {seed} #{i} mode={mode} D={d} heads={hq}/{hkv} R={requests} T={tokens} "
+            f"C={capacity} window={window} positions={positions.tolist()} fp8={fp8} chunk={chunk}")
+        slots, kc, vc, kn, vn, q = attention_case(rng, mode, requests, tokens, hq, hkv, d, capacity,
+                                                  positions)
+        if mode == 0:
+            got = run_attention(torch, 0, q, kc, vc, kn, vn, slots, positions, capacity, window,
+                                window + tokens - 1, chunk=chunk)
+            ref = oracle.verify_attention(q, kc, vc, kn, vn, slots, positions, capacity, window)
+        elif mode == 1 and fp8:
+            ks = float(np.abs(oracle.bf16_to_f32(kc)).max() / 448.0)
+            vs = float(np.abs(oracle.bf16_to_f32(vc)).max() / 448.0)
+            enc = lambda a, s: oracle.f32_to_e4m3(oracle.bf16_to_f32(a) / np.float32(s)).reshape(a.shape)
+            qk, qv, qkn, qvn = enc(kc, ks), enc(vc, vs), enc(kn, ks), enc(vn, vs)
+            got = run_attention(torch, 1, q, qk, qv, qkn, qvn, slots, positions, capacity, 0, capacity,
+                                fp8=True, k_scale=ks, v_scale=vs, chunk=chunk)
+            ref = oracle.verify_attention_fp8(q, qk, qv, qkn, qvn, ks, vs, slots, positions, capacity)
+        elif mode == 1:
+            got = run_attention(torch, 1, q, kc, vc, kn, vn, slots, positions, capacity, 0, capacity,
+                                chunk=chunk)
+            ref = oracle.verify_attention(q, kc, vc, kn, vn, slots, positions, capacity, 0)
+        else:
+            dummy = np.zeros((requests, 1, hkv, d), np.uint16)
+            got = run_attention(torch, 2, q, kc, vc, dummy, dummy, slots, positions, capacity, 0,
+                                capacity, chunk=chunk)[:, 0]
+            ref = oracle.decode_attention(q[:, 0], kc, vc, slots, positions, hkv, capacity)
+        err = attention_err(got, ref)
+        say(f"  max err / max ref = {err:.3e}")
+        assert err <= 2e-2, i
