@@ -687,3 +687,63 @@ def test_attention_random_shapes(dev, seed):
         err = attention_err(got, ref)
         say(f"  max err / max ref = {err:.3e}")
         assert err <= 2e-2, i
+
+
+def random_gemm_cases(seed, count):
+    """Seeded random fp8 GEMM calls: rows around the token-block edges (1-32 rows take two-tile
+    blocks, up to 128 one block, more several), K from one 128-byte step to 16, feature counts
+    that select the one-, two- and four-tile layouts, and every epilogue (bf16 store with amax,
+    split-K partials, GELU gate, argmax)."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(count):
+        epilogue = int(rng.choice([0, 1, 3, 2]))
+        m = int(rng.choice([1, 3, 16, 31, 32, 33, 100, 120, 128, 129, 200, 300]))
+        k = int(rng.choice([128, 384, 1024, 2048]))
+        if epilogue == 3:
+            n = int(rng.choice([128, 256, 1024, 8192, 16384]))
+        else:
+            n = int(rng.choice([64, 192, 320, 512, 1024, 8192, 16384]))
+        while m * n * k > 2_000_000_000:  # keep the float64 oracle quick
+            n //= 2
+        steps = k // 128
+        splits = int(rng.choice([s for s in (1, 2, 3, 4) if steps % s == 0])) if epilogue == 1 else 1
+        cases.append((i, epilogue, m, k, n, splits))
+    return cases
+
+
+@pytest.mark.parametrize("seed", [303, 404])
+def test_fp8_gemm_random_shapes(dev, seed):
+    """Sixteen seeded random fp8 GEMM calls per seed through the op-level entry point against the
+    oracle's float64 GEMM over the same e4m3 bytes: bf16 outputs within one bf16 ulp (plus 1e-3
+    of the maximum), split-K partials within fp32 reassociation, the GELU gate within 2e-2, and
+    the fused argmax bit-exact on the kernel's own logits and a near-tie of the oracle's."""
+    torch = dev
+    for i, epilogue, m, k, n, splits in random_gemm_cases(seed, 16):
+        rng = np.random.default_rng(seed * 1000 + i)
+        say(f"case: seed {seed} #{i} epilogue={epilogue} m={m} k={k} n={n} splits={splits}")
+        x = oracle.f32_to_bf16(rng.standard_normal((m, k)))
+        amax = float(np.abs(oracle.bf16_to_f32(x)).max())
+        qw, sw = rand_fp8(rng, (n, k), 0.05 if epilogue == 3 else 0.02)
+        qx, sx = oracle.quantize_e4m3(x)
+        if epilogue == 3:
+            y, y_amax, _, _ = run_fp8_linear(torch, x, amax, qw, sw, 3)
+            ref, _ = oracle.gelu_tanh_gate_rows(oracle.fp8_linear(qx, sx, qw, sw))
+            assert bf16_rel_err(y, ref) <= 2e-2, i
+            assert y_amax == np.abs(oracle.bf16_to_f32(y)).max(), i
+            continue
+        ref32 = oracle.fp8_linear_f32(qx, sx, qw, sw).astype(np.float64)
+        if epilogue == 1:
+            _, _, part, _ = run_fp8_linear(torch, x, amax, qw, sw, 1, splits)
+            summed = part.sum(0).astype(np.float64) * np.float32(sx * sw)
+            assert np.allclose(summed, ref32, rtol=1e-3, atol=1e-4 * np.abs(ref32).max()), i
+            continue
+        y, y_amax, _, _ = run_fp8_linear(torch, x, amax, qw, sw, 0)
+        gf = oracle.bf16_to_f32(y).astype(np.float64)
+        assert np.all(np.abs(gf - ref32) <= np.abs(ref32) * 2 ** -7 + 1e-3 * np.abs(ref32).max()), i
+        assert y_amax == np.abs(gf).max(), i
+        if epilogue == 2:
+            _, _, _, pred = run_fp8_linear(torch, x, amax, qw, sw, 2)
+            assert np.array_equal(pred, oracle.argmax_bf16_rows(y)), i
+            gap = ref32.max(1) - ref32[np.arange(m), pred]
+            assert np.all(gap <= 2 * 2 ** -7 * np.abs(ref32).max(1)), i
