@@ -535,3 +535,33 @@ def test_append_is_a_lock_step_decode(model):
     with pytest.raises(CaratError, match="token batch contains an invalid token id"):
         runner.append([0, 1, 2, desc.vocabulary])
     assert runner.position() == 61 and all(runner.slot_position(s) == 61 for s in range(BATCH))
+
+
+def test_seed_empty_cache_for_benchmark(model):
+    """seed_empty_cache_for_benchmark (batch_model_runner.cu:1845-1870): every cache row zeroed,
+    every slot at `position`, the reference's message for an out-of-range position; a verify step
+    over the zeroed caches then matches the oracle composition."""
+    desc, runner = model
+    runner.seed_random_cache(50, seed=15, stddev=1 / math.sqrt(128))
+    runner.seed_empty_cache_for_benchmark(37)
+    for li in range(len(desc.layers)):
+        assert not runner.read(f"cache.{li}.k", np.uint16).any()
+        assert not runner.read(f"cache.{li}.v", np.uint16).any()
+    assert [runner.slot_position(s) for s in range(BATCH)] == [37] * BATCH
+    with pytest.raises(CaratError, match="invalid benchmark cache position"):
+        runner.seed_empty_cache_for_benchmark(MAX_CONTEXT)
+    with pytest.raises(CaratError, match="invalid benchmark cache position"):
+        runner.seed_empty_cache_for_benchmark(-1)
+    rng = np.random.default_rng(23)
+    T = 5
+    props = rng.integers(0, desc.vocabulary, (BATCH, T)).astype(np.int32)
+    slots = list(range(BATCH))
+    positions = np.full(BATCH, 37, np.int32)
+    expect = verify_step(runner, desc, BATCH, capacity_of(desc), props, slots, positions)
+    say("case: verify over the zeroed benchmark cache")
+    runner.verify_greedy_proposals(props.tolist(), props[:, 0].tolist(), slots, [0] * BATCH)
+    pred = np.array(runner.last_predictions, np.int32)
+    logits = oracle.bf16_to_f32(expect["logits"]).astype(np.float64).reshape(BATCH * T, -1)
+    gap = logits.max(1) - logits[np.arange(BATCH * T), pred]
+    assert np.all(gap <= 2 * 2 ** -7 * np.abs(logits).max(1))
+    assert int(np.sum(pred != expect["predictions"])) <= max(1, BATCH * T // 10)
