@@ -553,7 +553,11 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-library-compare", action="store_true",
                     help="skip timing the vendor library (hipBLASLt) at the per-layer GEMM shapes")
-    ap.add_argument("--breakdown", action="store_true", help="probe every kernel kind (stderr)")
+    ap.add_argument("--assistant-fp8", choices=["off", "lm_head", "all"], default=None,
+                    help="the assistant's AssistantFp8Mode (default: CARAT_ASSISTANT_FP8_MODE, "
+                         "as the reference reads it; unset = off)")
+    ap.add_argument("--no-breakdown", action="store_true",
+                    help="skip the per-kernel-family probe of one verify step (kernels_ms_per_verify)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run one 256 MiB device-to-device copy (the reference kernel for "
                          "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
@@ -604,11 +608,16 @@ def main() -> int:
 
     desc = (ModelDesc.gemma4_31b(with_assistant=True) if args.native
             else ModelDesc.gemma4_benchmark(with_assistant=True))
+    desc.assistant_fp8_mode = args.assistant_fp8
+    assistant_fp8 = args.assistant_fp8 or os.environ.get("CARAT_ASSISTANT_FP8_MODE") or "off"
     total = args.warmup + args.steps
-    start_position = MAX_CONTEXT - DEPTH * (total + 2) - 8
+    # config 5's 8192-token contexts; the cache holds the rows the warmup, timed and probe steps
+    # add on top of them
+    start_position = MAX_CONTEXT
+    runner_context = MAX_CONTEXT + DEPTH * (total + 2) + 8
     rng = np.random.default_rng(args.seed)
     t0 = time.perf_counter()
-    runner = BatchModelRunner(desc, SLOTS, MAX_CONTEXT)
+    runner = BatchModelRunner(desc, SLOTS, runner_context)
     log(f"runner ready in {time.perf_counter() - t0:.1f}s; contexts start at {start_position}")
     slots = list(range(SLOTS))
     if args.seeded_cache:
@@ -655,7 +664,7 @@ def main() -> int:
     sliding_avg_ms, sliding_launches = runner.stream_gemm_probe("sliding_attention", passes=2)
 
     breakdown = {}
-    if args.breakdown:
+    if not args.no_breakdown:
         for kind in BatchModelRunner.PROBES:
             runner.set_probe(kind)
             runner.read_probe()
@@ -695,10 +704,11 @@ def main() -> int:
             "attention": ("sliding D256 32/16 heads, global D512 32/4 heads K=V" if args.native
                           else "D128 32/16 heads"),
             "slots": SLOTS, "draft": DRAFTS, "verify_rows": rows, "layers": 60,
-            "context_start": start_position, "accept_p": ACCEPT_P,
+            "context_start": start_position,
+            "context_capacity": runner_context, "accept_p": ACCEPT_P,
             "contexts": ("seeded KV values" if args.seeded_cache
                          else "prefilled from seeded random token ids"),
-            "graphs": bool(args.graphs),
+            "graphs": bool(args.graphs), "assistant_fp8_mode": assistant_fp8,
             "mean_accepted_per_step": round(accepted_total / steps, 2),
             "draft_ms": round(draft_ms / steps, 3), "verify_ms": round(verify_ms / steps, 3),
         },
@@ -759,7 +769,19 @@ def main() -> int:
     if not args.no_library_compare:
         add_library_times(gemms, SLOTS * DEPTH)  # last: it slows the kernels timed after it
     if breakdown:
-        result["kernels_ms_per_verify"] = breakdown
+        # one eager verify step per kernel family, hip events around every launch (the marker
+        # packets add a few us per launch)
+        result["kernels_ms_per_verify"] = dict(breakdown, rest={
+            "ms": round(verify_ms / steps - sum(v["ms"] for v in breakdown.values()), 3),
+            "what": "verify_ms minus the probed kernels: the row, quantisation, QKV and "
+                    "acceptance kernels and the kernel boundaries"})
+        gl = breakdown.get("global_attention")
+        if gl and gl["launches"]:
+            step_us = 1e3 * gl["ms"] / gl["launches"]
+            result["roofline"]["in_step"] = {
+                "avg_launch_us": round(step_us, 2),
+                "frac": round(attn_bytes / (step_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                "timing": "inside one verify step, hip events around each launch"}
     if not args.no_cpu_baseline and not args.native:
         log("cpu baseline (OpenMP oracle) ...")
         result["cpu_baseline"] = cpu_baseline(accepted_total / steps)

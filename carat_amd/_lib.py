@@ -48,7 +48,8 @@ class ModelDesc(ctypes.Structure):
                 ("sliding_window", c_int), ("rms_norm_epsilon", c_float), ("layer_count", c_int),
                 ("layers", POINTER(LayerDesc)), ("assistant", c_int), ("assistant_hidden", c_int),
                 ("assistant_intermediate", c_int), ("assistant_layers", c_int),
-                ("assistant_query_heads", c_int), ("seed", c_uint64), ("weight_std", c_float)]
+                ("assistant_query_heads", c_int), ("seed", c_uint64), ("weight_std", c_float),
+                ("assistant_fp8_mode", c_int)]
 
 
 class RowArgs(ctypes.Structure):

@@ -23,9 +23,11 @@ struct ArenaSet {
   const Fp8WeightArena *fp8[2];
 };
 
-// carat_hip_device_segment_fn over the reference's arenas: index 0 target, 1 assistant.
+// carat_hip_device_segment_fn over the reference's arenas: index 0 target, 1 assistant. The
+// arenas do not expose per-segment sizes, so *bytes is left as the runner's own figure; the
+// runner's description comes from the same Gemma4Config the arenas' WeightPlan was built from.
 const void *arena_segment(void *context, int assistant, int fp8, const char *name,
-                          const float **scale) {
+                          const float **scale, uint64_t * /*bytes*/) {
   const auto &arenas = *static_cast<const ArenaSet *>(context);
   const int which = assistant != 0 ? 1 : 0;
   try {
@@ -75,9 +77,11 @@ Gemma4BatchModelRunner::Gemma4BatchModelRunner(const Gemma4Config &config,
   desc.assistant_intermediate = static_cast<int>(assistant.intermediate);
   desc.assistant_layers = static_cast<int>(assistant.layers);
   desc.assistant_query_heads = static_cast<int>(assistant.query_heads);
-  // The assistant runs its projections in bf16 (AssistantFp8Mode::off); its FP8 arena, used by
-  // the reference's other assistant modes, is not read.
-  ArenaSet arenas{{&weights, assistant_weights}, {fp8_weights, nullptr}};
+  // The assistant's FP8 mode comes from CARAT_ASSISTANT_FP8_MODE, as in the reference's
+  // assistant runner (assistant_runner.cu:31-44); lm_head and all read the assistant FP8 arena
+  // and fail without it.
+  desc.assistant_fp8_mode = 0;
+  ArenaSet arenas{{&weights, assistant_weights}, {fp8_weights, assistant_fp8_weights}};
   hip_ok(carat_hip_runner_create_from_device_weights(&desc, arena_segment, &arenas, batch,
                                                      maximum_context, &runner_));
 }

@@ -98,6 +98,9 @@ ModelSpec spec_from_desc(const carat_hip_model_desc *d) {
   spec.assistant.intermediate = d->assistant_intermediate;
   spec.assistant.layers = d->assistant_layers;
   spec.assistant.query_heads = d->assistant_query_heads;
+  if (d->assistant_fp8_mode < 0 || d->assistant_fp8_mode > 3)
+    throw std::runtime_error("assistant_fp8_mode must be 0 (environment), 1 off, 2 lm_head or 3 all");
+  spec.assistant.fp8_mode = d->assistant_fp8_mode - 1;
   spec.seed = d->seed;
   spec.weight_std = d->weight_std;
   return spec;
@@ -459,9 +462,13 @@ int carat_hip_bench_speculative_cycle(carat_hip_runner *runner, int requests, in
     const std::vector<int> slot_list(slots, slots + requests);
     const std::vector<int> first(forced, forced + requests);
     std::vector<std::vector<int>> proposals(static_cast<size_t>(requests));
-    for (int i = 0; i < requests; ++i)
+    for (int i = 0; i < requests; ++i) {
       proposals[static_cast<size_t>(i)].assign(planted + static_cast<size_t>(i) * depth,
                                                planted + static_cast<size_t>(i + 1) * depth);
+      // the scheduler's proposals start with the token it forces (native_runtime_main.cpp:597-604)
+      if (planted[static_cast<size_t>(i) * depth] != forced[i])
+        throw std::runtime_error("planted proposals must start with the forced token");
+    }
     hip_check(hipDeviceSynchronize(), "synchronise before the speculative cycle");
     const auto start = std::chrono::steady_clock::now();
     // native_runtime_main.cpp:583-678: draft, caps from the proposals, verify, commit. The
@@ -474,13 +481,25 @@ int carat_hip_bench_speculative_cycle(carat_hip_runner *runner, int requests, in
     for (int i = 0; i < requests; ++i)
       caps[static_cast<size_t>(i)] = acceptance_cap(depth, remaining, proposals[static_cast<size_t>(i)], stops);
     const GreedyVerificationResult result = r.verify_greedy_proposals(proposals, first, slot_list, caps);
+    // Rows that accepted nothing append their forced token in one ragged decode step
+    // (native_runtime_main.cpp:636-646), which also yields their next token.
+    std::vector<int> fallback_slots, fallback_tokens;
+    for (int i = 0; i < requests; ++i)
+      if (result.accepted_tokens[static_cast<size_t>(i)] == 0) {
+        fallback_slots.push_back(slot_list[static_cast<size_t>(i)]);
+        fallback_tokens.push_back(first[static_cast<size_t>(i)]);
+      }
+    std::vector<int> fallback_next;
+    if (!fallback_slots.empty()) fallback_next = r.append_ragged(fallback_tokens, fallback_slots);
+    size_t fallback_index = 0;
     for (int i = 0; i < requests; ++i) {
       const int a = result.accepted_tokens[static_cast<size_t>(i)];
       const auto &row = proposals[static_cast<size_t>(i)];
       const std::span<const int> accepted_drafts(row.data() + 1, a > 1 ? static_cast<size_t>(a - 1) : 0);
+      const int next_token =
+          a == 0 ? fallback_next.at(fallback_index++) : result.next_tokens[static_cast<size_t>(i)];
       const SpeculativeCommit commit =
-          commit_speculation(first[static_cast<size_t>(i)], accepted_drafts,
-                             result.next_tokens[static_cast<size_t>(i)], stops);
+          commit_speculation(first[static_cast<size_t>(i)], accepted_drafts, next_token, stops);
       accepted_out[i] = a;
       next_out[i] = commit.next_token;
       last_out[i] = commit.resident_tokens.back();

@@ -190,9 +190,12 @@ __device__ __forceinline__ float amax_read(const float *amax, int stripes) {
 // last of those reads every stripe and releases the tensor's amax (bit 31 set) in the release
 // word, which the others poll. Arrivals on one address serialise, so the two-level count keeps
 // the chain short (measured on MI355X, one-shot kernels: +1.5 us at 120 workgroups and +1.8 us
-// at 224, against +2.0 and +3.3 us with a single counter). Agent-scope read-modify-writes are
-// coherent across the XCDs without cache maintenance, so no fence is needed: the only values
-// exchanged are these atomics. `sync` holds kFusedSyncWords words kAmaxStripeFloats floats apart
+// at 224, against +2.0 and +3.3 us with a single counter; measured with relaxed atomics). The
+// only values exchanged are these agent-scope atomics; the memory-model order comes from the
+// arrivals (acquire-release: each carries its workgroup's stripe update to the last arrival of
+// its counter and on to the global last arrival) and from the release word (written with release,
+// polled with acquire), so it does not rest on how the hardware happens to order relaxed
+// read-modify-writes to different addresses. `sync` holds kFusedSyncWords words kAmaxStripeFloats floats apart
 // (global counter, release word, eight counters), zeroed beforehand; `workgroups` is the number
 // that arrive. A wait past `spins` polls (kFusedQuantizeSpins in production, far beyond any real
 // wait) sets *fault (the result is then not to be used) and returns. The arriving workgroups must be resident at once, or the early ones wait
@@ -216,9 +219,9 @@ __device__ __forceinline__ float fused_amax_release(float *amax, int stripes, un
     const unsigned group_size = (workgroups - group + 7u) / 8u;  // workgroups of this counter
     const unsigned groups = workgroups < 8u ? workgroups : 8u;
     const unsigned arrived = __hip_atomic_fetch_add(sync + (2 + group) * kAmaxStripeFloats, 1u,
-                                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                                                    __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
     if (arrived + 1 == group_size)
-      last = __hip_atomic_fetch_add(sync, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1 == groups;
+      last = __hip_atomic_fetch_add(sync, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) + 1 == groups;
   }
   last = __shfl(last, 0, kWave);
   if (last) {
@@ -228,14 +231,14 @@ __device__ __forceinline__ float fused_amax_release(float *amax, int stripes, un
                        : 0u;
     const float total = wave_max(__uint_as_float(bits));
     if (lane == 0)
-      (void)__hip_atomic_exchange(release, __float_as_uint(total) | 0x80000000u, __ATOMIC_RELAXED,
+      (void)__hip_atomic_exchange(release, __float_as_uint(total) | 0x80000000u, __ATOMIC_RELEASE,
                                   __HIP_MEMORY_SCOPE_AGENT);
     return total;
   }
   unsigned seen = 0;
   if (lane == 0) {
     for (int spin = 0; spin < spins; ++spin) {
-      seen = __hip_atomic_fetch_or(release, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      seen = __hip_atomic_fetch_or(release, 0u, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
       if (seen & 0x80000000u) break;
       __builtin_amdgcn_s_sleep(2);
     }

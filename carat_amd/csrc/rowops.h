@@ -59,6 +59,11 @@ struct RowArgs {
 };
 constexpr int kFusedQuantizeRows = 192;  // every row's workgroup is resident at once (256 CUs)
 void launch_row_kernel(const RowArgs &args, hipStream_t stream);
+// Whether launch_row_kernel can quantise `args`'s output into the operand workspace (the
+// layer-end shape: split-K partials of an fp8 GEMM with 1-4 or 8 splits, both norms, a width
+// with a layer-end instance that is a multiple of 128, <= kFusedQuantizeRows rows, the output
+// amax, 2 or 8 token tiles). The xprep, sync and fault fields are not looked at.
+bool row_kernel_can_fuse_quantization(const RowArgs &args);
 
 // ---------------------------------------------------------------------------------------------
 // QKV post-processing (cuda/qkv.cu:387-530): reduces the QKV GEMM partials into the packed row,

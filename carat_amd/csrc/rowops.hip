@@ -602,24 +602,43 @@ __global__ __launch_bounds__(256) void argmax_accept_final_kernel(const ArgmaxAc
 }  // namespace
 
 namespace {
-// The layer-end shape of the verify step (see layer_end_kernel); false when it does not apply.
-bool launch_layer_end(const RowArgs &a, hipStream_t stream) {
+// The layer-end kernel's shape test (see layer_end_kernel): whether it serves `a`, whether the
+// partials carry fp8 scale operands, and its quads per thread (0: no instance for the width).
+struct LayerEndShape {
+  bool fixed = false;
+  bool scaled = false;
+  int q = 0;
+};
+
+LayerEndShape layer_end_shape(const RowArgs &a) {
+  LayerEndShape s;
   // fp8 projections' partials carry their scale operands; bf16 ones (the assistant) none
-  const bool scaled = a.x_amax != nullptr && a.w_scale != nullptr;
-  const bool fixed = a.source == RowSource::partials && (scaled || (a.x_amax == nullptr && a.w_scale == nullptr)) &&
-                     a.w1 != nullptr && a.residual != nullptr && a.r1_out != nullptr &&
-                     a.w2 != nullptr && a.y_out != nullptr && (a.y_amax != nullptr || !scaled) &&
-                     a.v_out == nullptr && a.rows < 512 &&
-                     ((a.splits >= 1 && a.splits <= 4) || a.splits == 8);
+  s.scaled = a.x_amax != nullptr && a.w_scale != nullptr;
+  s.fixed = a.source == RowSource::partials && (s.scaled || (a.x_amax == nullptr && a.w_scale == nullptr)) &&
+            a.w1 != nullptr && a.residual != nullptr && a.r1_out != nullptr &&
+            a.w2 != nullptr && a.y_out != nullptr && (a.y_amax != nullptr || !s.scaled) &&
+            a.v_out == nullptr && a.rows < 512 &&
+            ((a.splits >= 1 && a.splits <= 4) || a.splits == 8);
   const int quads = a.width / 4;
   // (quads per thread, threads): 5376 wide rows take 448 x 3 with no idle lane
-  const int q = a.width == 5376 ? 3 : quads <= 256 ? 5 : quads <= 1024 ? 1 : quads <= 2048 ? 2 : quads <= 4096 ? 4 : 0;
+  s.q = a.width == 5376 ? 3 : quads <= 256 ? 5 : quads <= 1024 ? 1 : quads <= 2048 ? 2 : quads <= 4096 ? 4 : 0;
+  return s;
+}
+
+bool fused_quantization_fits(const RowArgs &a, const LayerEndShape &s) {
+  return s.fixed && s.scaled && s.q != 0 && a.rows <= kFusedQuantizeRows && a.y_amax != nullptr &&
+         a.width % 128 == 0 && (a.xprep_token_tiles == 2 || a.xprep_token_tiles == 8);
+}
+
+// The layer-end shape of the verify step (see layer_end_kernel); false when it does not apply.
+bool launch_layer_end(const RowArgs &a, hipStream_t stream) {
+  const LayerEndShape shape = layer_end_shape(a);
+  const bool scaled = shape.scaled;
+  const int q = shape.q;
   if (a.xprep != nullptr &&
-      (!fixed || !scaled || q == 0 || a.rows > kFusedQuantizeRows || a.sync == nullptr ||
-       a.fault == nullptr || a.y_amax == nullptr || a.width % 128 != 0 ||
-       (a.xprep_token_tiles != 2 && a.xprep_token_tiles != 8)))
+      (!fused_quantization_fits(a, shape) || a.sync == nullptr || a.fault == nullptr))
     throw std::runtime_error("fused row quantisation needs the layer-end shape, <= 192 rows and its sync words");
-  if (!fixed || q == 0) return false;
+  if (!shape.fixed || q == 0) return false;
   auto go = [&](auto quads_per_thread, auto threads) {
     constexpr int Q = decltype(quads_per_thread)::value;
     constexpr int T = decltype(threads)::value;
@@ -646,6 +665,10 @@ bool launch_layer_end(const RowArgs &a, hipStream_t stream) {
   return true;
 }
 }  // namespace
+
+bool row_kernel_can_fuse_quantization(const RowArgs &a) {
+  return fused_quantization_fits(a, layer_end_shape(a));
+}
 
 void launch_row_kernel(const RowArgs &a, hipStream_t stream) {
   if (a.rows <= 0 || a.width <= 0) throw std::runtime_error("invalid row kernel shape");

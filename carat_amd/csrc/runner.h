@@ -32,6 +32,10 @@ struct AssistantSpec {
   int intermediate = 8192;
   int layers = 4;          // layers 0..layers-2 sliding, the last global (assistant_runner.cu:162-169)
   int query_heads = 32;
+  // AssistantFp8Mode (assistant_runner.cu:29-43): 0 off (bf16 projections), 1 lm_head (the
+  // draft lm_head in e4m3), 2 all (every projection in e4m3, inputs quantised per tensor);
+  // -1 reads CARAT_ASSISTANT_FP8_MODE as the reference does (unset: off).
+  int fp8_mode = -1;
 };
 
 struct ModelSpec {
@@ -87,10 +91,12 @@ public:
   // address of the execution segment the reference's WeightPlan names `name`
   // (weight_plan.cpp:37-189), laid out as that plan lays it out: bf16 when fp8 == 0; e4m3 with
   // its per-tensor scale (a device float stored to *scale) when fp8 == 1, or null, in which
-  // case the runner quantises the bf16 segment per tensor (amax/448) itself. Segments are copied
-  // device to device and packed; they are only read during construction.
+  // case the runner quantises the bf16 segment per tensor (amax/448) itself. *bytes holds the
+  // size the runner expects on entry; the source stores the segment's own size there when it
+  // knows it, and a different size is an error (nothing is copied). Segments are copied device
+  // to device and packed; they are only read during construction.
   using DeviceSegmentFn = const void *(*)(void *context, int assistant, int fp8, const char *name,
-                                          const float **scale);
+                                          const float **scale, uint64_t *bytes);
   BatchModelRunner(const ModelSpec &spec, DeviceSegmentFn segment, void *context, int batch,
                    int maximum_context);
   ~BatchModelRunner();

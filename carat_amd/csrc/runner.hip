@@ -119,14 +119,21 @@ struct AssistantLayer {
   int attention_chunk = 0;  // keys per workgroup of its decode attention over the target cache
   DeviceBuffer input_norm, q_norm, post_attention_norm, pre_mlp_norm, post_mlp_norm, scalar;
   PackedWeight q, o, gate_up, down;  // bf16
+  // AssistantFp8Mode::all: e4m3 copies (per-tensor scales: q, o, gate_up, down)
+  PackedWeight q8, o8, gate_up8, down8;
+  DeviceBuffer scales8;
 };
 
+// [embedding(token) * bf16(sqrt(H)) | previous hidden] (embedding_batch_bf16 +
+// concatenate_rows_bf16, assistant_runner.cu:289-293); with `amax`, also the striped amax of the
+// row (the quantisation of the pre-projection input in AssistantFp8Mode::all).
 __global__ void assistant_input_kernel(const bf16_t *embedding, const int32_t *tokens,
                                        const bf16_t *previous, bf16_t *out, int rows, int hidden,
-                                       int vocabulary, float scale) {
+                                       int vocabulary, float scale, float *amax, int stripes) {
   const int row = blockIdx.y;
   const bf16_t s = f32_to_bf16(scale);
   const int token = tokens[row];
+  float maximum = 0.0f;
   for (int c = blockIdx.x * blockDim.x + threadIdx.x; c < 2 * hidden; c += gridDim.x * blockDim.x) {
     bf16_t v;
     if (c < hidden)
@@ -137,7 +144,11 @@ __global__ void assistant_input_kernel(const bf16_t *embedding, const int32_t *t
     else
       v = previous[static_cast<size_t>(row) * hidden + (c - hidden)];
     out[static_cast<size_t>(row) * 2 * hidden + c] = v;
+    maximum = fmaxf(maximum, fabsf(bf16_to_f32(v)));
   }
+  if (amax == nullptr) return;  // uniform over the launch
+  maximum = wave_max(maximum);
+  if ((threadIdx.x & (kWave - 1)) == 0) amax_publish(amax, stripes, maximum);
 }
 
 __global__ void gather_rows_kernel(const bf16_t *in, const int32_t *rows_index, bf16_t *out,
@@ -223,6 +234,12 @@ struct BatchModelRunner::Implementation {
   std::vector<AssistantLayer> assistant_layers;
   PackedWeight a_embedding, a_pre_projection, a_post_projection;  // bf16
   DeviceBuffer a_final_norm;
+  // AssistantFp8Mode (assistant_runner.cu:29-43): 0 off, 1 lm_head, 2 all. The e4m3 copies of
+  // the lm_head (both fp8 modes) and of the pre/post projections (all), per-tensor scales
+  // [lm_head, pre, post]; per-draft-step striped amaxes of the projections' inputs.
+  int assistant_fp8 = 0;
+  PackedWeight a_embedding8, a_pre_projection8, a_post_projection8;
+  DeviceBuffer a_scales8, a_amax;
   DeviceBuffer a_input, a_hidden_a, a_hidden_b, a_normalized, a_first_residual, a_pre_mlp,
       a_activated, a_queries, a_attention_out, a_final_hidden, a_previous_hidden;
   DeviceBuffer a_io;
@@ -327,15 +344,25 @@ struct BatchModelRunner::Implementation {
   // selects the assistant's plan).
   bool has_source() const { return checkpoint != nullptr || device_segment != nullptr; }
 
+  // A device segment whose owner reported a size other than the runner's (a description that
+  // disagrees with the arena) would be read out of bounds: refuse it before any copy.
+  static void check_segment_bytes(const std::string &name, uint64_t reported, size_t expected) {
+    if (reported != expected)
+      throw std::runtime_error("device weight " + name + " has " + std::to_string(reported) +
+                               " bytes, the runner expects " + std::to_string(expected));
+  }
+
   void upload_segment(const std::string &name, void *device, size_t bytes) {
     const bool assistant = name.rfind("assistant.", 0) == 0;
     const std::string segment = assistant ? name.substr(10) : name;
     if (device_segment != nullptr) {
-      const void *source =
-          device_segment(device_segment_context, assistant ? 1 : 0, 0, segment.c_str(), nullptr);
+      uint64_t source_bytes = bytes;
+      const void *source = device_segment(device_segment_context, assistant ? 1 : 0, 0,
+                                          segment.c_str(), nullptr, &source_bytes);
       if (source == nullptr)
         throw std::runtime_error(std::string(assistant ? "assistant" : "target") +
                                  " device weights have no segment " + segment);
+      check_segment_bytes(name, source_bytes, bytes);
       hip_check(hipMemcpyAsync(device, source, bytes, hipMemcpyDeviceToDevice, stream),
                 "copy device weight segment");
       return;
@@ -380,9 +407,11 @@ struct BatchModelRunner::Implementation {
     const bool assistant = name.rfind("assistant.", 0) == 0;
     const std::string segment = assistant ? name.substr(10) : name;
     const float *source_scale = nullptr;
+    uint64_t source_bytes = bytes;
     const void *source = device_segment(device_segment_context, assistant ? 1 : 0, 1,
-                                        segment.c_str(), &source_scale);
+                                        segment.c_str(), &source_scale, &source_bytes);
     if (source == nullptr) return false;
+    check_segment_bytes(name + " (e4m3)", source_bytes, bytes);
     if (source_scale == nullptr)
       throw std::runtime_error("device fp8 weight " + segment + " has no scale");
     hip_check(hipMemcpyAsync(dst, source, bytes, hipMemcpyDeviceToDevice, stream),
@@ -430,9 +459,13 @@ struct BatchModelRunner::Implementation {
     pack_from_staging(w, n, k, gate_up);
   }
 
-  // bf16 weight [n][k], stored packed.
+  // bf16 weight [n][k], stored packed. With `fp8`, also its e4m3 copy with a per-tensor scale
+  // into *fp8_scale: the device source's own (Fp8WeightArena, required when loading from device
+  // segments), else the bf16 values quantised per tensor (amax/448) as Fp8WeightArena::quantize
+  // does (device_weights.cu:200-263).
   void fill_bf16_weight(PackedWeight &w, int n, int k, bool gate_up, uint64_t tensor,
-                        float stddev, const std::string &segment) {
+                        float stddev, const std::string &segment, PackedWeight *fp8 = nullptr,
+                        float *fp8_scale = nullptr) {
     const size_t count = static_cast<size_t>(n) * k;
     void *dst = staging_for(count * sizeof(bf16_t));
     if (has_source())
@@ -440,6 +473,49 @@ struct BatchModelRunner::Implementation {
     else
       fill_normal_bf16(static_cast<bf16_t *>(dst), count, seed_for(tensor), 0.0f, stddev, stream);
     pack_from_staging(w, n, 2 * k, gate_up);
+    if (fp8 == nullptr) return;
+    if (load_staging.bytes() < count) {
+      hip_check(hipStreamSynchronize(stream), "synchronise before staging growth");
+      load_staging.release();
+      load_staging.allocate(count * sizeof(bf16_t));
+    }
+    fp8_t *e4m3 = load_staging.as<fp8_t>();
+    if (!copy_device_fp8(segment, e4m3, count, fp8_scale)) {
+      if (device_segment != nullptr)
+        throw std::runtime_error("assistant FP8 mode requires quantized assistant weights");
+      quantize_weight_bf16_to_fp8(static_cast<const bf16_t *>(dst), e4m3, count, fp8_scale,
+                                  init_scratch.as<float>(), stream);
+    }
+    fp8->layout = gemm_weight_layout(n, k, gate_up);
+    fp8->data.allocate(count);
+    pack_weight(e4m3, fp8->data.get(), fp8->layout, stream);
+  }
+
+  // AssistantFp8Mode of the assistant runner (assistant_runner.cu:31-44): the description's,
+  // or CARAT_ASSISTANT_FP8_MODE. Quantized weights exist unless the runner loads device
+  // segments whose source has no assistant e4m3 arena.
+  int resolve_assistant_fp8_mode() {
+    bool quantized = true;
+    if (device_segment != nullptr) {
+      const float *scale = nullptr;
+      uint64_t bytes = static_cast<uint64_t>(spec.vocabulary) * spec.assistant.hidden;
+      quantized = device_segment(device_segment_context, 1, 1, "token_embedding", &scale,
+                                 &bytes) != nullptr;
+    }
+    int mode = spec.assistant.fp8_mode;
+    if (mode < 0) {
+      const char *configured = std::getenv("CARAT_ASSISTANT_FP8_MODE");
+      const std::string text = configured == nullptr ? "off" : configured;
+      if (text == "off") return 0;
+      if (!quantized) throw std::runtime_error("assistant FP8 mode requires quantized assistant weights");
+      if (text == "lm_head") return 1;
+      if (text == "all") return 2;
+      throw std::runtime_error("CARAT_ASSISTANT_FP8_MODE must be off, lm_head or all");
+    }
+    if (mode > 2) throw std::runtime_error("invalid assistant FP8 mode");
+    if (mode != 0 && !quantized)
+      throw std::runtime_error("assistant FP8 mode requires quantized assistant weights");
+    return mode;
   }
 
   void fill_bf16(DeviceBuffer &buffer, size_t n, uint64_t tensor, float stddev,
@@ -537,6 +613,8 @@ struct BatchModelRunner::Implementation {
     const size_t AI = static_cast<size_t>(as.intermediate);
     const size_t H = static_cast<size_t>(spec.hidden);
     uint64_t tensor = 50000;
+    assistant_fp8 = resolve_assistant_fp8_mode();
+    const bool all8 = assistant_fp8 == 2;
     assistant_layers.resize(static_cast<size_t>(as.layers));
     for (int i = 0; i < as.layers; ++i) {
       AssistantLayer &L = assistant_layers[static_cast<size_t>(i)];
@@ -554,17 +632,37 @@ struct BatchModelRunner::Implementation {
       fill_norm(L.pre_mlp_norm, as.hidden, tensor++, p + "pre_mlp_norm");
       fill_norm(L.post_mlp_norm, as.hidden, tensor++, p + "post_mlp_norm");
       fill_norm(L.scalar, 1, tensor++, p + "scalar");
-      fill_bf16_weight(L.q, static_cast<int>(qw), as.hidden, false, tensor++, sd, p + "q");
-      fill_bf16_weight(L.o, as.hidden, static_cast<int>(qw), false, tensor++, sd, p + "o");
-      fill_bf16_weight(L.gate_up, 2 * as.intermediate, as.hidden, true, tensor++, sd, p + "gate_up");
-      fill_bf16_weight(L.down, as.hidden, as.intermediate, false, tensor++, sd, p + "down");
+      float *scales8 = nullptr;
+      if (all8) {
+        L.scales8.allocate(4 * sizeof(float));
+        scales8 = L.scales8.as<float>();
+      }
+      fill_bf16_weight(L.q, static_cast<int>(qw), as.hidden, false, tensor++, sd, p + "q",
+                       all8 ? &L.q8 : nullptr, scales8);
+      fill_bf16_weight(L.o, as.hidden, static_cast<int>(qw), false, tensor++, sd, p + "o",
+                       all8 ? &L.o8 : nullptr, all8 ? scales8 + 1 : nullptr);
+      fill_bf16_weight(L.gate_up, 2 * as.intermediate, as.hidden, true, tensor++, sd, p + "gate_up",
+                       all8 ? &L.gate_up8 : nullptr, all8 ? scales8 + 2 : nullptr);
+      fill_bf16_weight(L.down, as.hidden, as.intermediate, false, tensor++, sd, p + "down",
+                       all8 ? &L.down8 : nullptr, all8 ? scales8 + 3 : nullptr);
+    }
+    float *scales8 = nullptr;
+    if (assistant_fp8 != 0) {
+      a_scales8.allocate(3 * sizeof(float));
+      scales8 = a_scales8.as<float>();
     }
     fill_bf16_weight(a_embedding, spec.vocabulary, as.hidden, false, tensor++, spec.weight_std,
-                     "assistant.token_embedding");
+                     "assistant.token_embedding", assistant_fp8 != 0 ? &a_embedding8 : nullptr,
+                     scales8);
     fill_bf16_weight(a_pre_projection, as.hidden, 2 * spec.hidden, false, tensor++,
-                     spec.weight_std, "assistant.pre_projection");
+                     spec.weight_std, "assistant.pre_projection", all8 ? &a_pre_projection8 : nullptr,
+                     all8 ? scales8 + 1 : nullptr);
     fill_bf16_weight(a_post_projection, spec.hidden, as.hidden, false, tensor++, spec.weight_std,
-                     "assistant.post_projection");
+                     "assistant.post_projection", all8 ? &a_post_projection8 : nullptr,
+                     all8 ? scales8 + 2 : nullptr);
+    if (assistant_fp8 != 0)
+      a_amax.allocate(sizeof(float) * static_cast<size_t>(kMaximumDepth) *
+                      assistant_amax_slots_per_step() * kAmaxSlotFloats);
     fill_norm(a_final_norm, as.hidden, tensor++, "assistant.final_norm");
     const size_t B = static_cast<size_t>(batch_size);
     size_t max_qw = 0;
@@ -617,6 +715,15 @@ struct BatchModelRunner::Implementation {
         partial = std::max(partial, gemm_partial_floats(L.q, batch_size));
         partial = std::max(partial, gemm_partial_floats(L.o, batch_size));
         partial = std::max(partial, gemm_partial_floats(L.down, batch_size));
+        if (assistant_fp8 == 2) {
+          partial = std::max(partial, gemm_partial_floats(L.q8, batch_size));
+          partial = std::max(partial, gemm_partial_floats(L.o8, batch_size));
+          partial = std::max(partial, gemm_partial_floats(L.down8, batch_size));
+        }
+      }
+      if (assistant_fp8 == 2) {
+        partial = std::max(partial, gemm_partial_floats(a_pre_projection8, batch_size));
+        partial = std::max(partial, gemm_partial_floats(a_post_projection8, batch_size));
       }
     }
     hidden_a.allocate(sizeof(bf16_t) * M * H);
@@ -636,9 +743,17 @@ struct BatchModelRunner::Implementation {
       size_t xp = std::max(gemm_xprep_bytes(step_rows, spec.hidden),
                            gemm_xprep_bytes(step_rows, spec.intermediate));
       for (auto &L : layers) xp = std::max(xp, gemm_xprep_bytes(step_rows, L.query_width()));
+      if (assistant_fp8 != 0) {
+        const AssistantSpec &as = spec.assistant;
+        for (const int k : {2 * spec.hidden, as.hidden, as.intermediate})
+          xp = std::max(xp, gemm_xprep_bytes(batch_size, k));
+        for (auto &L : assistant_layers)
+          xp = std::max(xp, gemm_xprep_bytes(batch_size, as.query_heads * L.head_dimension));
+      }
       xprep.allocate(xp);
       size_t keys = gemm_argmax_partials(step_rows, lm_head.layout);
       if (has_assistant) keys = std::max(keys, gemm_argmax_partials(batch_size, a_embedding.layout));
+      if (assistant_fp8 != 0) keys = std::max(keys, gemm_argmax_partials(batch_size, a_embedding8.layout));
       argmax_partials.allocate(sizeof(uint64_t) * keys);
     }
     target_hidden.allocate(sizeof(bf16_t) * static_cast<size_t>(batch_size) * H);
@@ -890,14 +1005,16 @@ struct BatchModelRunner::Implementation {
   // Returns whether next_normalized also went out quantised into the xprep workspace.
   bool enqueue_layer(size_t li, const StepIo &io, bf16_t *next_normalized, float *next_amax) {
     const int rows = io.requests * io.depth;
-    const bool fuse = io.fused_quantize && rows <= kFusedQuantizeRows;
+    // Each layer-end row quantises its output only where the row kernel has the fused shape
+    // (otherwise the next GEMM prepares its operand itself, with the same bytes).
     auto fuse_quantize = [&](RowArgs &r, int which) {
-      if (!fuse) return;
-      r.xprep = xprep.as<unsigned char>();
       r.xprep_token_tiles = gemm_token_tiles(rows);
+      if (!io.fused_quantize || !row_kernel_can_fuse_quantization(r)) return false;
+      r.xprep = xprep.as<unsigned char>();
       r.sync = sync_slot(li, which);
       r.fault = d_fault;
       r.quantize_spins = fused_quantize_mode == 2 ? 0 : kFusedQuantizeSpins;
+      return true;
     };
     TargetLayer &L = layers[li];
     const float *scales = L.scales.as<float>();
@@ -961,12 +1078,13 @@ struct BatchModelRunner::Implementation {
     ro.w2 = L.pre_mlp_norm.as<bf16_t>();
     ro.y_out = pre_mlp.as<bf16_t>();
     ro.y_amax = amax_slot(li, 2);
-    fuse_quantize(ro, 0);
+    const bool pre_mlp_prepared = fuse_quantize(ro, 0);
     launch_row_kernel(ro, stream);
     // gate/up with the GELU gate fused
     run_fp8_gemm(pre_mlp.as<bf16_t>(), rows, spec.hidden, amax_slot(li, 2), L.gate_up,
                  scales + 2, GemmEpilogue::gelu_gate,
-                 activated.as<bf16_t>(), amax_slot(li, 3), nullptr, probe_gate_up_gemm, fuse);
+                 activated.as<bf16_t>(), amax_slot(li, 3), nullptr, probe_gate_up_gemm,
+                 pre_mlp_prepared);
     // down + post-MLP norm + residual + layer scalar + next input norm
     run_fp8_gemm(activated.as<bf16_t>(), rows, spec.intermediate, amax_slot(li, 3),
                  L.down, scales + 3, GemmEpilogue::partial_f32, nullptr,
@@ -989,9 +1107,9 @@ struct BatchModelRunner::Implementation {
                                     : layers[li + 1].input_norm.as<bf16_t>();
     rd.y_out = next_normalized;
     rd.y_amax = next_amax;
-    fuse_quantize(rd, 1);
+    const bool next_prepared = fuse_quantize(rd, 1);
     launch_row_kernel(rd, stream);
-    return fuse;
+    return next_prepared;
   }
 
   void enqueue_embedding(const int32_t *tokens, int rows, bf16_t *hidden, bf16_t *normalized_out,
@@ -1063,10 +1181,11 @@ struct BatchModelRunner::Implementation {
     for (size_t li = 0; li < layers.size(); ++li) {
       io.in_amax = amax_slot(li, 0);
       const bool last = li + 1 == layers.size();
-      io.input_prepared = enqueue_layer(li, io, last ? final_hidden.as<bf16_t>() : normalized.as<bf16_t>(),
-                                        last ? lm_head_amax() : amax_slot(li + 1, 0)) &&
-                          !last;
-      if (last) last_input_prepared = io.fused_quantize && rows <= kFusedQuantizeRows;
+      const bool prepared = enqueue_layer(
+          li, io, last ? final_hidden.as<bf16_t>() : normalized.as<bf16_t>(),
+          last ? lm_head_amax() : amax_slot(li + 1, 0));
+      io.input_prepared = prepared && !last;
+      if (last) last_input_prepared = prepared;
       std::swap(io.input, io.output);
     }
     // lm_head + argmax (a forced prefill step whose predictions nobody reads skips it; the
@@ -1528,15 +1647,53 @@ struct BatchModelRunner::Implementation {
   }
 
   // -------------------------------------------------------------------------------- draft
+  // Striped amaxes of one draft step's projection inputs (fp8 modes): the pre-projection input,
+  // then per layer its normalized input, attention output, pre-MLP row and GELU output, then the
+  // final hidden row (the lm_head and post-projection input).
+  size_t assistant_amax_slots_per_step() const { return 2 + 4 * spec.assistant.layers; }
+  float *assistant_amax(int step, size_t which) {
+    if (assistant_fp8 == 0) return nullptr;
+    return a_amax.as<float>() +
+           (static_cast<size_t>(step) * assistant_amax_slots_per_step() + which) * kAmaxSlotFloats;
+  }
+  // Layer li's amax slot k (0 normalized input, 1 attention output, 2 pre-MLP, 3 GELU output)
+  // in `all` mode, else null (the bf16 projections need none).
+  float *assistant_layer_amax(int step, size_t li, int k) {
+    return assistant_fp8 == 2 ? assistant_amax(step, 1 + 4 * li + static_cast<size_t>(k)) : nullptr;
+  }
+  float *assistant_final_amax(int step) {
+    return assistant_amax(step, assistant_amax_slots_per_step() - 1);
+  }
+
+  // One assistant projection into split-K partials: bf16 (Bf16Linear), or in `all` mode the e4m3
+  // copy with the input quantised per tensor from its amax (run_linear's Fp8Linear path,
+  // assistant_runner.cu:147-160). Returns the split count.
+  int run_assistant_partial(const bf16_t *x, int rows, int k, const PackedWeight &w,
+                            const PackedWeight &w8, const float *w8_scale, const float *x_amax) {
+    if (assistant_fp8 != 2) return run_bf16_gemm_partial(x, rows, k, w);
+    int splits = 1;
+    run_fp8_gemm(x, rows, k, x_amax, w8, w8_scale, GemmEpilogue::partial_f32, nullptr, nullptr,
+                 &splits, probe_none);
+    return splits;
+  }
+
   void run_assistant_layer(size_t li, const bf16_t *input, bf16_t *output, int active, int step,
                            bool last_layer) {
     const AssistantSpec &as = spec.assistant;
     AssistantLayer &L = assistant_layers[li];
     const TargetLayer &target = layers[static_cast<size_t>(L.global ? last_global : last_sliding)];
     const int qw = as.query_heads * L.head_dimension;
-    int splits = run_bf16_gemm_partial(a_normalized.as<bf16_t>(), active, as.hidden,
-                                       L.q);
+    const bool all8 = assistant_fp8 == 2;
+    const float *scales8 = all8 ? L.scales8.as<float>() : nullptr;
+    const int stripes = assistant_fp8 != 0 ? kAmaxStripes : 1;
+    int splits = run_assistant_partial(a_normalized.as<bf16_t>(), active, as.hidden, L.q, L.q8,
+                                       scales8, assistant_layer_amax(step, li, 0));
     QkvArgs q;
+    q.amax_stripes = stripes;
+    if (all8) {
+      q.x_amax = assistant_layer_amax(step, li, 0);
+      q.w_scale = scales8;
+    }
     q.partials = partials.as<float>();
     q.splits = splits;
     q.rows = active;
@@ -1568,11 +1725,19 @@ struct BatchModelRunner::Implementation {
     at.capacity = target.capacity;
     at.max_keys = target.capacity;
     at.out = a_attention_out.as<bf16_t>();
+    at.out_amax = assistant_layer_amax(step, li, 1);
+    at.amax_stripes = stripes;
     at.partials = attention_partials.as<float>();
     at.chunk_keys = L.attention_chunk;
     launch_attention(at, stream);
-    splits = run_bf16_gemm_partial(a_attention_out.as<bf16_t>(), active, qw, L.o);
+    splits = run_assistant_partial(a_attention_out.as<bf16_t>(), active, qw, L.o, L.o8,
+                                   all8 ? scales8 + 1 : nullptr, assistant_layer_amax(step, li, 1));
     RowArgs ro;
+    ro.amax_stripes = stripes;
+    if (all8) {
+      ro.x_amax = assistant_layer_amax(step, li, 1);
+      ro.w_scale = scales8 + 1;
+    }
     ro.source = RowSource::partials;
     ro.rows = active;
     ro.width = as.hidden;
@@ -1584,22 +1749,35 @@ struct BatchModelRunner::Implementation {
     ro.r1_out = a_first_residual.as<bf16_t>();
     ro.w2 = L.pre_mlp_norm.as<bf16_t>();
     ro.y_out = a_pre_mlp.as<bf16_t>();
+    ro.y_amax = assistant_layer_amax(step, li, 2);
     launch_row_kernel(ro, stream);
-    GemmArgs g;
-    g.x = a_pre_mlp.as<bf16_t>();
-    g.ldx = as.hidden;
-    g.m = active;
-    g.k = as.hidden;
-    g.w = L.gate_up.get();
-    g.n = 2 * as.intermediate;
-    g.w_layout = L.gate_up.layout;
-    g.epilogue = GemmEpilogue::gelu_gate;
-    g.y = a_activated.as<bf16_t>();
-    g.ldy = as.intermediate;
-    launch_bf16_gemm(g, stream);
-    splits = run_bf16_gemm_partial(a_activated.as<bf16_t>(), active, as.intermediate,
-                                   L.down);
+    if (all8) {
+      run_fp8_gemm(a_pre_mlp.as<bf16_t>(), active, as.hidden, assistant_layer_amax(step, li, 2),
+                   L.gate_up8, scales8 + 2, GemmEpilogue::gelu_gate, a_activated.as<bf16_t>(),
+                   assistant_layer_amax(step, li, 3), nullptr, probe_none);
+    } else {
+      GemmArgs g;
+      g.x = a_pre_mlp.as<bf16_t>();
+      g.ldx = as.hidden;
+      g.m = active;
+      g.k = as.hidden;
+      g.w = L.gate_up.get();
+      g.n = 2 * as.intermediate;
+      g.w_layout = L.gate_up.layout;
+      g.epilogue = GemmEpilogue::gelu_gate;
+      g.y = a_activated.as<bf16_t>();
+      g.ldy = as.intermediate;
+      launch_bf16_gemm(g, stream);
+    }
+    splits = run_assistant_partial(a_activated.as<bf16_t>(), active, as.intermediate, L.down,
+                                   L.down8, all8 ? scales8 + 3 : nullptr,
+                                   assistant_layer_amax(step, li, 3));
     RowArgs rd;
+    rd.amax_stripes = stripes;
+    if (all8) {
+      rd.x_amax = assistant_layer_amax(step, li, 3);
+      rd.w_scale = scales8 + 3;
+    }
     rd.source = RowSource::partials;
     rd.rows = active;
     rd.width = as.hidden;
@@ -1612,6 +1790,7 @@ struct BatchModelRunner::Implementation {
     rd.r1_out = output;
     rd.w2 = last_layer ? a_final_norm.as<bf16_t>() : assistant_layers[li + 1].input_norm.as<bf16_t>();
     rd.y_out = last_layer ? a_final_hidden.as<bf16_t>() : a_normalized.as<bf16_t>();
+    rd.y_amax = last_layer ? assistant_final_amax(step) : assistant_layer_amax(step, li + 1, 0);
     launch_row_kernel(rd, stream);
   }
 
@@ -1652,6 +1831,12 @@ struct BatchModelRunner::Implementation {
     hip_check(hipEventRecord(start_event, stream), "record draft start");
     const AssistantSpec &as = spec.assistant;
     const int H = spec.hidden;
+    const bool all8 = assistant_fp8 == 2;
+    const int stripes = assistant_fp8 != 0 ? kAmaxStripes : 1;
+    if (assistant_fp8 != 0)
+      launch_step_init(a_amax.as<float>(),
+                       static_cast<int>(depth * assistant_amax_slots_per_step() * kAmaxStripes),
+                       stream);
     {
       // previous_hidden = target_hidden_by_slot[slots]
       const dim3 grid(std::max(1, std::min(32, (H + 255) / 256)), active);
@@ -1665,12 +1850,20 @@ struct BatchModelRunner::Implementation {
         const dim3 grid(std::max(1, std::min(64, (2 * H + 255) / 256)), active);
         assistant_input_kernel<<<grid, 256, 0, stream>>>(
             embedding_bf16.as<bf16_t>(), input_tokens, a_previous_hidden.as<bf16_t>(),
-            a_input.as<bf16_t>(), active, H, spec.vocabulary, std::sqrt(static_cast<float>(H)));
+            a_input.as<bf16_t>(), active, H, spec.vocabulary, std::sqrt(static_cast<float>(H)),
+            all8 ? assistant_amax(d, 0) : nullptr, stripes);
         hip_check(hipGetLastError(), "launch assistant input");
       }
-      int splits = run_bf16_gemm_partial(a_input.as<bf16_t>(), active, 2 * H,
-                                         a_pre_projection);
+      int splits = run_assistant_partial(a_input.as<bf16_t>(), active, 2 * H, a_pre_projection,
+                                         a_pre_projection8,
+                                         all8 ? a_scales8.as<float>() + 1 : nullptr,
+                                         all8 ? assistant_amax(d, 0) : nullptr);
       RowArgs rp;
+      rp.amax_stripes = stripes;
+      if (all8) {
+        rp.x_amax = assistant_amax(d, 0);
+        rp.w_scale = a_scales8.as<float>() + 1;
+      }
       rp.source = RowSource::partials;
       rp.rows = active;
       rp.width = as.hidden;
@@ -1680,6 +1873,7 @@ struct BatchModelRunner::Implementation {
       rp.v_out = a_hidden_a.as<bf16_t>();
       rp.w2 = assistant_layers[0].input_norm.as<bf16_t>();
       rp.y_out = a_normalized.as<bf16_t>();
+      rp.y_amax = assistant_layer_amax(d, 0, 0);
       launch_row_kernel(rp, stream);
       bf16_t *input = a_hidden_a.as<bf16_t>();
       bf16_t *output = a_hidden_b.as<bf16_t>();
@@ -1701,6 +1895,16 @@ struct BatchModelRunner::Implementation {
         g.w = a_embedding.get();
         g.n = spec.vocabulary;
         g.w_layout = a_embedding.layout;
+        if (assistant_fp8 != 0) {
+          // Fp8Linear over the e4m3 lm_head, the final hidden row quantised per tensor
+          g.w = a_embedding8.get();
+          g.w_layout = a_embedding8.layout;
+          g.x_amax = assistant_final_amax(d);
+          g.w_scale = a_scales8.as<float>();
+          g.amax_stripes = kAmaxStripes;
+          g.xprep = xprep.as<unsigned char>();
+          g.xprep_capacity = xprep.bytes();
+        }
         g.epilogue = GemmEpilogue::argmax;
         g.argmax_partials = argmax_partials.as<uint64_t>();
         g.argmax_partial_capacity = argmax_partials.bytes() / sizeof(uint64_t);
@@ -1708,11 +1912,21 @@ struct BatchModelRunner::Implementation {
         g.argmax_table = a_proposals;
         g.argmax_table_stride = depth;
         g.argmax_table_column = d;
-        launch_bf16_gemm(g, stream);
+        if (assistant_fp8 != 0)
+          launch_fp8_gemm(g, stream);
+        else
+          launch_bf16_gemm(g, stream);
       }
-      splits = run_bf16_gemm_partial(a_final_hidden.as<bf16_t>(), active, as.hidden,
-                                     a_post_projection);
+      splits = run_assistant_partial(a_final_hidden.as<bf16_t>(), active, as.hidden,
+                                     a_post_projection, a_post_projection8,
+                                     all8 ? a_scales8.as<float>() + 2 : nullptr,
+                                     assistant_final_amax(d));
       RowArgs rq;
+      rq.amax_stripes = stripes;
+      if (all8) {
+        rq.x_amax = assistant_final_amax(d);
+        rq.w_scale = a_scales8.as<float>() + 2;
+      }
       rq.source = RowSource::partials;
       rq.rows = active;
       rq.width = H;
@@ -1741,6 +1955,7 @@ struct BatchModelRunner::Implementation {
   void *tensor(const std::string &name, size_t *bytes, WeightLayout *layout = nullptr) {
     if (layout != nullptr) *layout = WeightLayout{};
     auto give = [&](const DeviceBuffer &b) {
+      if (b.get() == nullptr) throw std::runtime_error("runner tensor is not allocated: " + name);
       if (bytes != nullptr) *bytes = b.bytes();
       return b.get();
     };
@@ -1762,8 +1977,25 @@ struct BatchModelRunner::Implementation {
     if (name == "assistant.pre_projection") return give_packed(a_pre_projection);
     if (name == "assistant.post_projection") return give_packed(a_post_projection);
     if (name == "assistant.final_norm") return give(a_final_norm);
+    // AssistantFp8Mode e4m3 copies (absent when the mode does not use them) and their scales
+    // [lm_head, pre_projection, post_projection]
+    if (name == "assistant.token_embedding.fp8") return give_packed(a_embedding8);
+    if (name == "assistant.pre_projection.fp8") return give_packed(a_pre_projection8);
+    if (name == "assistant.post_projection.fp8") return give_packed(a_post_projection8);
+    if (name == "assistant.fp8_scales") return give(a_scales8);
     // the last draft step's post-projection output ([batch][hidden] bf16, rows < active valid)
     if (name == "assistant.previous_hidden") return give(a_previous_hidden);
+    // the last draft step's intermediates, as the last assistant layer left them (rows < active)
+    if (name == "assistant.input") return give(a_input);  // [embedding | previous hidden]
+    if (name == "assistant.hidden_a") return give(a_hidden_a);
+    if (name == "assistant.hidden_b") return give(a_hidden_b);
+    if (name == "assistant.normalized") return give(a_normalized);
+    if (name == "assistant.queries") return give(a_queries);
+    if (name == "assistant.attention_out") return give(a_attention_out);
+    if (name == "assistant.first_residual") return give(a_first_residual);
+    if (name == "assistant.pre_mlp") return give(a_pre_mlp);
+    if (name == "assistant.activated") return give(a_activated);
+    if (name == "assistant.final_hidden") return give(a_final_hidden);
     const auto dot = name.find('.');
     const auto dot2 = name.find('.', dot + 1);
     if (dot != std::string::npos && dot2 != std::string::npos) {
@@ -1786,6 +2018,11 @@ struct BatchModelRunner::Implementation {
             if (field == "down") return give_packed(L.down);
             if (field == "post_mlp_norm") return give(L.post_mlp_norm);
             if (field == "scalar") return give(L.scalar);
+            if (field == "q.fp8") return give_packed(L.q8);
+            if (field == "o.fp8") return give_packed(L.o8);
+            if (field == "gate_up.fp8") return give_packed(L.gate_up8);
+            if (field == "down.fp8") return give_packed(L.down8);
+            if (field == "fp8_scales") return give(L.scales8);  // [q, o, gate_up, down]
           }
         }
       } else {

@@ -39,6 +39,9 @@ class ModelDesc:
     assistant_query_heads: int = 32
     seed: int = 1
     weight_std: float = 0.02
+    # AssistantFp8Mode (assistant_runner.cu:29-43): None reads CARAT_ASSISTANT_FP8_MODE as the
+    # reference does (unset: off); else "off", "lm_head" or "all"
+    assistant_fp8_mode: str | None = None
 
     @staticmethod
     def gemma4_benchmark(with_assistant: bool = True) -> "ModelDesc":
@@ -68,6 +71,10 @@ class ModelDesc:
         d.assistant_hidden, d.assistant_intermediate = self.assistant_hidden, self.assistant_intermediate
         d.assistant_layers, d.assistant_query_heads = self.assistant_layers, self.assistant_query_heads
         d.seed, d.weight_std = self.seed, self.weight_std
+        modes = {None: 0, "off": 1, "lm_head": 2, "all": 3}
+        if self.assistant_fp8_mode not in modes:
+            raise ValueError("assistant_fp8_mode must be None, 'off', 'lm_head' or 'all'")
+        d.assistant_fp8_mode = modes[self.assistant_fp8_mode]
         return d, arr
 
 
@@ -151,26 +158,33 @@ class BatchModelRunner:
         return acc, nxt, last, seconds.value
 
     SEGMENT_FN = ctypes.CFUNCTYPE(ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
-                                  ctypes.c_char_p, ctypes.POINTER(ctypes.c_void_p))
+                                  ctypes.c_char_p, ctypes.POINTER(ctypes.c_void_p),
+                                  ctypes.POINTER(ctypes.c_uint64))
 
     @classmethod
     def from_device_weights(cls, desc: ModelDesc, segments: dict, batch: int, maximum_context: int,
                             fp8_segments: dict | None = None) -> "BatchModelRunner":
         """The runner over weights already on the device (DeviceWeightArena / Fp8WeightArena,
         device_weights.h:15-52). `segments` maps (assistant, name) to the device address of the
-        bf16 execution segment the reference's WeightPlan calls `name`; `fp8_segments` (optional)
-        maps it to (e4m3 segment address, device address of its fp32 scale)."""
+        bf16 execution segment the reference's WeightPlan calls `name`, or to (address, byte
+        size); `fp8_segments` (optional) maps it to (e4m3 segment address, device address of its
+        fp32 scale[, byte size]). A byte size that differs from the runner's is an error."""
         fp8_segments = fp8_segments or {}
 
-        def lookup(_context, assistant, fp8, name, scale):
+        def lookup(_context, assistant, fp8, name, scale, size):
             key = (bool(assistant), name.decode())
+            entry = fp8_segments.get(key) if fp8 else segments.get(key)
+            if entry is None:
+                return None
             if fp8:
-                entry = fp8_segments.get(key)
-                if entry is None:
-                    return None
                 scale[0] = entry[1]
+                if len(entry) > 2:
+                    size[0] = entry[2]
                 return entry[0]
-            return segments.get(key)
+            if isinstance(entry, tuple):
+                size[0] = entry[1]
+                return entry[0]
+            return entry
 
         callback = cls.SEGMENT_FN(lookup)
         self = cls.__new__(cls)

@@ -73,6 +73,14 @@ typedef struct carat_hip_model_desc {
   int assistant_query_heads;
   uint64_t seed;               /* seeded synthetic weights */
   float weight_std;
+  /* AssistantFp8Mode (assistant_runner.cu:29-43): 0 reads CARAT_ASSISTANT_FP8_MODE as the
+   * reference's assistant runner does (unset = off), 1 off, 2 lm_head, 3 all. A mode other than
+   * off needs quantized assistant weights: the seeded and checkpoint runners quantise the
+   * assistant's matrices per tensor themselves (as the reference's loader does when the mode is
+   * on, native_runtime_main.cpp:926-933); a runner over device weights takes them from the
+   * assistant FP8 arena (segment(..., assistant = 1, fp8 = 1, ...)) and otherwise fails with
+   * "assistant FP8 mode requires quantized assistant weights". */
+  int assistant_fp8_mode;
 } carat_hip_model_desc;
 
 typedef struct carat_hip_runner carat_hip_runner;
@@ -109,11 +117,15 @@ int carat_hip_runner_create_from_checkpoint(const char *model_dir, const char *a
  * `name` ("token_embedding", "layer.3.qkv", ...; weight_plan.cpp:37-189; assistant = 1 selects
  * the assistant's plan) -- bf16 when fp8 == 0; when fp8 == 1 its e4m3 copy with the per-tensor
  * scale's device address stored to *scale, or NULL, and the runner then quantises the bf16
- * segment per tensor (amax/448) itself. Segments are copied device to device during
- * construction (the arenas may be freed afterwards) and packed. desc gives the shapes; its seed
- * and weight_std are unused. */
+ * segment per tensor (amax/448) itself. *bytes holds the segment size the runner expects on
+ * entry: the callback stores the segment's own byte size there when it knows it, and a size
+ * that differs fails the construction before anything is copied ("device weight <name> has N
+ * bytes, the runner expects M"). Segments are copied device to device during construction (the
+ * arenas may be freed afterwards) and packed. desc gives the shapes; its seed and weight_std
+ * are unused. */
 typedef const void *(*carat_hip_device_segment_fn)(void *context, int assistant, int fp8,
-                                                   const char *name, const float **scale);
+                                                   const char *name, const float **scale,
+                                                   uint64_t *bytes);
 int carat_hip_runner_create_from_device_weights(const carat_hip_model_desc *desc,
                                                 carat_hip_device_segment_fn segment,
                                                 void *context, int batch, int maximum_context,
@@ -210,8 +222,10 @@ int carat_hip_runner_timing(carat_hip_runner *runner, float *verify_ms, float *d
  * acceptance_cap per request over `planted` [requests][depth] (the benchmark's proposals, row 0
  * = forced, which replace the drafts), verify_greedy_proposals over them with those caps,
  * commit_speculation per
- * request -- timed on the host clock from a synchronised device (*seconds_out). Writes the
- * accepted counts, the next forced token and the last resident token of every request. */
+ * request, after one append_ragged of the forced tokens of the requests that accepted nothing
+ * (the scheduler's fallback, which gives their next token) -- timed on the host clock from a
+ * synchronised device (*seconds_out). Every planted row must start with its forced token. Writes
+ * the accepted counts, the next forced token and the last resident token of every request. */
 int carat_hip_bench_speculative_cycle(carat_hip_runner *runner, int requests, int depth,
                                       const int32_t *last_tokens, const int32_t *slots,
                                       const int32_t *forced, const int32_t *planted,

@@ -89,8 +89,11 @@ def _shared_layers(desc):
 
 
 def draft_steps(runner, desc, batch, capacity_of, last_tokens, slots, forced=None, depth=4,
-                feed=None):
-    """One draft_four call (assistant_runner.cu:218-338), bf16 projections (AssistantFp8Mode::off).
+                feed=None, fp8_mode="off"):
+    """One draft_four call (assistant_runner.cu:218-338) in AssistantFp8Mode `fp8_mode`: "off"
+    runs every projection in bf16; "lm_head" runs the lm_head, and "all" every projection, as an
+    e4m3 GEMM over the runner's e4m3 weight copies with the input quantised per tensor from its
+    own amax (run_linear, :147-160: quantize_bf16_to_fp8_e4m3 then Fp8Linear).
 
     Per step: input = [embedding(token) * bf16(sqrt(H)) | previous hidden], pre-projection, the
     assistant layers (run_layer, :162-208: q-only projection, query RMSNorm + RoPE at position
@@ -114,6 +117,20 @@ def draft_steps(runner, desc, batch, capacity_of, last_tokens, slots, forced=Non
     post_w = runner.read("assistant.post_projection", np.uint16).reshape(H, AH)
     final_norm = runner.read("assistant.final_norm", np.uint16)
     previous = runner.read("target_hidden", np.uint16).reshape(batch, H)[slots]
+    all8 = fp8_mode == "all"
+    if fp8_mode != "off":
+        scales8 = runner.read("assistant.fp8_scales", np.float32)
+        a_emb8 = runner.read("assistant.token_embedding.fp8", np.uint8).reshape(desc.vocabulary, AH)
+    if all8:
+        pre_w8 = runner.read("assistant.pre_projection.fp8", np.uint8).reshape(AH, 2 * H)
+        post_w8 = runner.read("assistant.post_projection.fp8", np.uint8).reshape(H, AH)
+
+    def linear(x, w, w8=None, s8=None):
+        if w8 is None:
+            return oracle.bf16_linear(x, w)
+        qx, sx = oracle.quantize_e4m3(x)
+        return oracle.fp8_linear(qx, sx, w8, float(s8))
+
     last_sliding, last_global = _shared_layers(desc)
     layers = []
     for li in range(desc.assistant_layers):
@@ -129,6 +146,9 @@ def draft_steps(runner, desc, batch, capacity_of, last_tokens, slots, forced=Non
         w["o"] = runner.read(pre + "o", np.uint16).reshape(AH, hq * D)
         w["gate_up"] = runner.read(pre + "gate_up", np.uint16).reshape(2 * desc.assistant_intermediate, AH)
         w["down"] = runner.read(pre + "down", np.uint16).reshape(AH, desc.assistant_intermediate)
+        for n in ("q", "o", "gate_up", "down"):
+            w[n + "8"] = (runner.read(pre + n + ".fp8", np.uint8).reshape(w[n].shape) if all8 else None)
+        w["s8"] = runner.read(pre + "fp8_scales", np.float32) if all8 else [None] * 4
         kind = "global" if glob else "sliding"
         w["cos"] = runner.read(f"rope.{kind}.cos", np.uint16).reshape(-1, D)
         w["sin"] = runner.read(f"rope.{kind}.sin", np.uint16).reshape(-1, D)
@@ -139,30 +159,34 @@ def draft_steps(runner, desc, batch, capacity_of, last_tokens, slots, forced=Non
     out = {"tokens": np.zeros((rows, depth), np.int32), "logits": [], "hidden": []}
     for d in range(depth):
         x = oracle.embedding(emb, tokens, math.sqrt(H))
-        h = oracle.bf16_linear(np.concatenate([x, previous], axis=1), pre_w)
+        h = linear(np.concatenate([x, previous], axis=1), pre_w, pre_w8 if all8 else None,
+                   scales8[1] if all8 else None)
         for w, D, hkv, hq, C in layers:
             n, _ = oracle.rms_norm(h, w["input_norm"], eps=desc.rms_norm_epsilon)
-            qp = oracle.bf16_linear(n, w["q"])
+            qp = linear(n, w["q"], w["q8"], w["s8"][0])
             q, _, _ = oracle.qkv_post(qp, w["q_norm"], w["q_norm"], w["cos"], w["sin"], context + d,
                                       hq, 0, D, False, desc.rms_norm_epsilon)
             attn = oracle.decode_attention(q, w["k"], w["v"], slots, context, hkv, C)
-            o = oracle.bf16_linear(attn.reshape(rows, hq * D), w["o"])
+            o = linear(attn.reshape(rows, hq * D), w["o"], w["o8"], w["s8"][1])
             r1, pre_mlp, _ = oracle.rms_norm_add_and_norm(o, w["post_attention_norm"], h,
                                                           w["pre_mlp_norm"], desc.rms_norm_epsilon)
-            act, _ = oracle.gelu_tanh_gate_rows(oracle.bf16_linear(pre_mlp, w["gate_up"]))
-            down = oracle.bf16_linear(act, w["down"])
+            act, _ = oracle.gelu_tanh_gate_rows(linear(pre_mlp, w["gate_up"], w["gate_up8"], w["s8"][2]))
+            down = linear(act, w["down"], w["down8"], w["s8"][3])
             h = oracle.rms_norm_add_scale(down, w["post_mlp_norm"], r1, int(w["scalar"][0]),
                                           desc.rms_norm_epsilon)
         fh, _ = oracle.rms_norm(h, final_norm, eps=desc.rms_norm_epsilon)
         if d == 0 and forced is not None:
             step_tokens = np.asarray(forced, np.int32)
             out["logits"].append(None)
+        elif fp8_mode != "off":
+            step_tokens, logits = oracle.fp8_lm_head_argmax(fh, a_emb8, float(scales8[0]))
+            out["logits"].append(logits)
         else:
             logits = oracle.bf16_linear(fh, a_emb)
             step_tokens = oracle.argmax_bf16_rows(logits)
             out["logits"].append(logits)
         out["tokens"][:, d] = step_tokens
-        previous = oracle.bf16_linear(fh, post_w)
+        previous = linear(fh, post_w, post_w8 if all8 else None, scales8[2] if all8 else None)
         out["hidden"].append(previous)
         tokens = step_tokens if feed is None else np.asarray(feed, np.int32)[:, d]
     return out

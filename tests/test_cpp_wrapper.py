@@ -2,7 +2,9 @@
 the reference's speculation helpers against its golden vectors on the CPU, and (GPU) a tiny
 runner driven through the reference's class interface."""
 import json
+import os
 import subprocess
+import sys
 from pathlib import Path
 
 import pytest
@@ -44,8 +46,29 @@ def test_cpp_wrapper_speculation_helpers(tmp_path):
     assert f"{n} speculation cases, 0 failures" in out.stdout
 
 
+def gpu_initialised_here() -> bool:
+    """Whether this process has opened the GPU: the HIP runtime opens /dev/kfd when it
+    initialises (torch's lazy CUDA init, or any HIP call through the library)."""
+    torch = sys.modules.get("torch")
+    if torch is not None and torch.cuda.is_initialized():
+        return True
+    fd_dir = Path("/proc/self/fd")
+    for fd in fd_dir.iterdir() if fd_dir.exists() else ():
+        try:
+            if os.readlink(fd) == "/dev/kfd":
+                return True
+        except OSError:
+            continue
+    return False
+
+
 @pytest.mark.gpu
 def test_cpp_wrapper_runner(tmp_path):
+    # The runner program is started as a child process; a process that has initialised the GPU
+    # must not fork and exec another program, so this test has to run before any GPU call here.
+    if gpu_initialised_here():
+        pytest.fail("test_cpp_wrapper_runner must run before this pytest process touches the GPU: "
+                    "run it first or in a process of its own")
     exe = build(tmp_path)
     print("case: C++ wrapper runner program", flush=True)
     out = subprocess.run([str(exe), "runner"], capture_output=True, text=True, timeout=110)

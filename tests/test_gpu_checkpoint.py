@@ -217,3 +217,58 @@ def test_runner_from_device_weights_equals_checkpoint_runner(loaded, torch_cuda)
     with pytest.raises(Exception, match="device weights have no segment final_norm"):
         BatchModelRunner.from_device_weights(
             desc, {k: v for k, v in addresses.items() if k != (False, "final_norm")}, BATCH, MAX_CONTEXT)
+    # a segment shorter than the description expects is refused before any copy reads past it
+    short = dict(addresses)
+    qkv = (False, "layer.0.qkv")
+    short[qkv] = (addresses[qkv], dev[qkv].numel() * 2 - 128)
+    with pytest.raises(Exception, match=r"device weight layer\.0\.qkv has \d+ bytes, the runner expects"):
+        BatchModelRunner.from_device_weights(desc, short, BATCH, MAX_CONTEXT)
+    sized = {k: (v, dev[k].numel() * 2) for k, v in addresses.items()}
+    BatchModelRunner.from_device_weights(desc, sized, BATCH, MAX_CONTEXT).close()
+
+
+def test_assistant_fp8_arena_from_device_weights(loaded, torch_cuda, monkeypatch):
+    """Gemma4BatchModelRunner(..., assistant_weights, assistant_fp8_weights) in the assistant's FP8
+    modes (assistant_runner.cu:29-43): the runner takes the assistant's e4m3 segments and scales
+    from the assistant FP8 arena (here the oracle's quantisation at twice the scale, so they
+    differ from what the runner would compute), and fails with the reference's error when a mode
+    is set and the arena is absent."""
+    torch = torch_cuda
+    runner, cfg, tensors, a_tensors = loaded
+    desc = runner._desc
+    host = plan_segments(cfg, tensors, a_tensors)
+    dev = {k: torch.from_numpy(np.ascontiguousarray(v).view(np.int16)).cuda() for k, v in host.items()}
+    addresses = {k: v.data_ptr() for k, v in dev.items()}
+    monkeypatch.setenv("CARAT_ASSISTANT_FP8_MODE", "all")
+    with pytest.raises(Exception, match="assistant FP8 mode requires quantized assistant weights"):
+        BatchModelRunner.from_device_weights(desc, addresses, BATCH, MAX_CONTEXT)
+    fp8, keep = {}, []
+    for (assistant, name), m in host.items():
+        if not assistant or m.ndim != 2 or "norm" in name:
+            continue
+        amax = float(np.abs(oracle.bf16_to_f32(m)).max())
+        q, s = oracle.quantize_e4m3(m, amax * 2.0)
+        dq = torch.from_numpy(np.ascontiguousarray(q)).cuda()
+        ds = torch.tensor([s], dtype=torch.float32, device="cuda")
+        keep += [dq, ds]
+        fp8[(True, name)] = (dq.data_ptr(), ds.data_ptr(), q.size, q, s)
+    say("case: runner from device weights with the assistant FP8 arena (mode all, from the environment)")
+    other = BatchModelRunner.from_device_weights(desc, addresses, BATCH, MAX_CONTEXT,
+                                                 {k: v[:3] for k, v in fp8.items()})
+    try:
+        scales = other.read("assistant.fp8_scales", np.float32)
+        for j, name in enumerate(("token_embedding", "pre_projection", "post_projection")):
+            q, s = fp8[(True, name)][3:]
+            assert np.array_equal(other.read(f"assistant.{name}.fp8", np.uint8), q.reshape(-1)), name
+            assert scales[j] == np.float32(s), name
+        for li in range(desc.assistant_layers):
+            ls = other.read(f"assistant.layer.{li}.fp8_scales", np.float32)
+            for j, n in enumerate(("q", "o", "gate_up", "down")):
+                q, s = fp8[(True, f"layer.{li}.{n}")][3:]
+                assert np.array_equal(other.read(f"assistant.layer.{li}.{n}.fp8", np.uint8), q.reshape(-1))
+                assert ls[j] == np.float32(s)
+        other.seed_random_cache(60, seed=23, stddev=1 / math.sqrt(128))
+        drafts = other.draft_four([1, 2, 3, 4], [0, 1, 2, 3], [5, 6, 7, 8], 4)
+        assert [row[0] for row in drafts] == [5, 6, 7, 8]
+    finally:
+        other.close()

@@ -375,6 +375,51 @@ def test_config5_draft_step_full_dimensions(full_model):
     assert err <= 2e-2
 
 
+@pytest.mark.parametrize("mode", ["lm_head", "all"])
+def test_config5_draft_fp8_modes_full_dimensions(torch_cuda, mode):
+    """The full-size assistant in AssistantFp8Mode lm_head / all (assistant_runner.cu:29-43,
+    147-160) over the 24 slots' caches: a forced step and one free step against the oracle chain
+    of the same mode, teacher-forced on the GPU's tokens."""
+    desc = full_desc()
+    desc.assistant_fp8_mode = mode
+    say(f"case: full-dimension runner create, assistant fp8 mode {mode}")
+    runner = BatchModelRunner(desc, SLOTS, MAX_CONTEXT)
+    try:
+        rng = np.random.default_rng(58)
+        positions = rng.integers(1024, MAX_CONTEXT - T + 1, SLOTS).astype(np.int32)
+        runner.seed_random_cache(int(positions.max()), seed=8, stddev=1 / math.sqrt(128))
+        for slot, p in enumerate(positions):
+            runner.set_slot_position(slot, int(p))
+        slots = rng.permutation(SLOTS).astype(np.int32).tolist()
+        last = rng.integers(0, VOCAB, SLOTS).astype(np.int32).tolist()
+        forced = rng.integers(0, VOCAB, SLOTS).astype(np.int32).tolist()
+        say(f"case: config-5 draft {mode} (depth 2, forced first token)")
+        got = np.array(runner.draft_four(last, slots, forced, 2), np.int32)
+        assert got[:, 0].tolist() == forced
+        exp = draft_steps(runner, desc, SLOTS, capacity_of(desc), last, slots, forced, 2, feed=got,
+                          fp8_mode=mode)
+        logits = oracle.bf16_to_f32(exp["logits"][1]).astype(np.float64)
+        gap = logits.max(1) - logits[np.arange(SLOTS), got[:, 1]]
+        mism = int(np.sum(got[:, 1] != exp["tokens"][:, 1]))
+        say(f"  draft {mode} argmax mismatches vs oracle {mism}/{SLOTS}, max gap {gap.max():.3e}")
+        assert np.all(gap <= 2 * 2 ** -7 * np.abs(logits).max(1))
+        assert mism <= 2
+        hidden = runner.read("assistant.previous_hidden", np.uint16).reshape(SLOTS, H)
+        g = oracle.bf16_to_f32(hidden).astype(np.float64)
+        e = oracle.bf16_to_f32(exp["hidden"][-1]).astype(np.float64)
+        err = np.abs(g - e).max() / np.abs(e).max()
+        mean_err = np.abs(g - e).mean() / np.abs(e).max()
+        say(f"  draft {mode} hidden hand-off max rel err {err:.2e}, mean {mean_err:.2e}")
+        # lm_head mode keeps bf16 projections (2e-2); in `all` an element whose bf16 input
+        # differs by an ulp can take the neighbouring e4m3 code in each projection, which the
+        # following projections spread (6e-2; test_gpu_runner.py holds each e4m3 stage to two
+        # bf16 ulps given its GPU inputs)
+        tolerance = 6e-2 if mode == "all" else 2e-2
+        assert err <= tolerance and mean_err <= tolerance / 5
+    finally:
+        runner.close()
+
+
 def test_config5_append_ragged_full_dimensions(full_model):
     """append_ragged (batch_model_runner.cu:1544-1615) over all 24 slots at config-5 dimensions:
     a depth-1 step of 24 rows, which takes the GEMMs' small-M kernels (two 16-token tiles) at the

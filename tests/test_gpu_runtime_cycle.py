@@ -149,6 +149,19 @@ def test_bench_cycle_equals_the_python_cycle(torch_cuda):
             assert nxt.tolist() == want_next and lst.tolist() == want_last
             assert [a.slot_position(s) for s in slots] == [b.slot_position(s) for s in slots]
             forced, last = nxt, lst
+        bad = planted.copy()
+        bad[:, 0] = forced + 1
+        with pytest.raises(Exception, match="planted proposals must start with the forced token"):
+            a.bench_speculative_cycle(last, slots, forced, bad, 3, [7])
+        # remaining = 0 caps every request at 0: nothing is accepted, and every request takes the
+        # scheduler's fallback (append_ragged of its forced token), as the Python cycle does
+        planted[:, 0] = forced
+        before = [a.slot_position(s) for s in slots]
+        acc, nxt, lst, _ = a.bench_speculative_cycle(last, slots, forced, planted, 0, [7])
+        want = b.append_ragged(forced.tolist(), slots)
+        assert acc.tolist() == [0] * BATCH
+        assert nxt.tolist() == want and lst.tolist() == forced.tolist()
+        assert [a.slot_position(s) for s in slots] == [p + 1 for p in before]
     finally:
         a.close()
         b.close()

@@ -60,3 +60,41 @@ def test_noalloc_argmax_accept_matches_workspace_entry(torch_cuda, bf16):
         exp_acc, exp_next = oracle.greedy_accept(proposals, first, arg, caps)
         assert np.array_equal(got[0], arg.reshape(-1))
         assert np.array_equal(got[1], exp_acc) and np.array_equal(got[2], exp_next)
+
+
+def test_noalloc_argmax_accept_scratch_limit(torch_cuda):
+    """The fixed scratch holds 65536 partial keys: 256 requests x 8 rows at vocabulary 262144 in
+    fp32 (32 chunks of 8192 per row) fill it exactly and match the workspace entry point; one
+    request more is rejected with the scratch error before anything runs (outputs untouched)."""
+    torch = torch_cuda
+    vocab, tokens = 262144, 8
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    stream = _lib.ptr(torch.cuda.current_stream().cuda_stream)
+    for requests in (256, 257):
+        say(f"case: no-alloc scratch limit {requests}x{tokens}x{vocab} fp32")
+        logits = torch.randn((requests * tokens, vocab), generator=gen, device="cuda")
+        proposals = torch.randint(0, vocab, (requests, tokens), generator=gen, device="cuda",
+                                  dtype=torch.int32)
+        first = proposals[:, 0].contiguous()
+        outs = {}
+        for entry in ("carat_hip_argmax_accept", "carat_hip_argmax_accept_noalloc"):
+            pred = torch.full((requests * tokens,), -7, dtype=torch.int32, device="cuda")
+            acc = torch.full((requests,), -7, dtype=torch.int32, device="cuda")
+            nxt = torch.full((requests,), -7, dtype=torch.int32, device="cuda")
+            status = getattr(_lib.lib(), entry)(
+                _lib.ptr(logits), None, requests, tokens, vocab, _lib.ptr(proposals),
+                _lib.ptr(first), None, _lib.ptr(pred), _lib.ptr(acc), _lib.ptr(nxt), stream)
+            torch.cuda.synchronize()
+            outs[entry] = (status, pred.cpu().numpy(), acc.cpu().numpy(), nxt.cpu().numpy())
+        status, *got = outs["carat_hip_argmax_accept_noalloc"]
+        want = outs["carat_hip_argmax_accept"]
+        assert want[0] == 0
+        if requests == 256:
+            assert status == 0
+            for a, b in zip(got, want[1:]):
+                assert np.array_equal(a, b)
+        else:
+            assert status != 0
+            assert "exceed the fixed scratch of 65536" in _lib.lib().carat_hip_last_error().decode()
+            assert all(np.all(a == -7) for a in got)
+        del logits
