@@ -29,7 +29,7 @@ EXPORTED = [
     "carat_hip_runner_reset_slot", "carat_hip_runner_seed_empty_cache_for_benchmark",
     "carat_hip_runner_seed_random_cache", "carat_hip_runner_set_slot_position",
     "carat_hip_runner_tensor", "carat_hip_runner_copy_tensor", "carat_hip_runner_set_graphs",
-    "carat_hip_runner_set_fused_quantization",
+    "carat_hip_runner_set_fused_quantization", "carat_hip_runner_set_qkv_fusion",
     "carat_hip_runner_timing", "carat_hip_runner_set_probe", "carat_hip_runner_read_probe",
     "carat_hip_runner_stream_gemm_probe", "carat_hip_bench_speculative_cycle",
     "carat_hip_argmax_accept", "carat_hip_argmax_accept_noalloc", "carat_hip_gemm_plan", "carat_hip_fp8_linear",

@@ -49,6 +49,13 @@ struct AttentionArgs {
   int chunk_keys = 0;               // keys per workgroup (multiple of 256; 0 = choose)
   hipEvent_t timing_start = nullptr;  // optional events around the main kernel (timing probes)
   hipEvent_t timing_stop = nullptr;
+  // Verify steps: the QKV post-processing of the step (launch_qkv_post's work, `qkv` its
+  // arguments over the projection's split-K partials) done by the attention kernel itself, each
+  // workgroup for its (request, kv head): the query rows go straight into the workgroup, this
+  // step's K/V rows (and a global layer's cache rows) are written before any key is read, and
+  // `q` is not read. Only where attention_can_fuse_qkv holds.
+  bool fuse_qkv = false;
+  QkvArgs qkv;
 };
 
 size_t attention_partials_floats(int requests, int kv_heads, int max_keys, int chunk_keys,
@@ -56,5 +63,10 @@ size_t attention_partials_floats(int requests, int kv_heads, int max_keys, int c
 int attention_default_chunk(AttentionMode mode, int max_keys, int requests, int kv_heads,
                             bool fp8_kv = false, int dimension = 128);
 void launch_attention(const AttentionArgs &args, hipStream_t stream);
+// Whether launch_attention can run `args` with fuse_qkv: a verify step (sliding or global) at
+// D = 128 with bf16 K/V, <= 16 query rows per kv head and <= 8 tokens, one key chunk per
+// (request, kv head), and `qkv` the matching QKV post-processing over 1-4 split-K partials of an
+// fp8 projection, with no position offset.
+bool attention_can_fuse_qkv(const AttentionArgs &args);
 
 }  // namespace carat_hip

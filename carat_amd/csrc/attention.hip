@@ -75,7 +75,141 @@ __device__ __forceinline__ KeyRange key_range(const AttentionArgs &a, int p) {
 template <int D, int NQ>
 constexpr int kAttentionOccupancy = D <= 128 ? (NQ == 1 ? 3 : 2) : D <= 256 ? 2 : 1;
 
-template <int D, int NQ, bool kFp8, AttentionMode kMode, int kWaves>
+// The QKV post-processing of one (request r, kv head h) inside the attention kernel, with the
+// arithmetic of qkv_post_kernel (cuda/qkv.cu:387-530) unit for unit, so the results are the same
+// bits: a unit is one (row, head) of the packed projection -- the G query heads of kv head h and
+// its K and V heads, for each of the request's T rows -- handled by one wave, lane l owning
+// elements 2l, 2l + 1; units go round-robin over the waves. load() issues every load of the
+// wave's units (split-K partials, norm weights, RoPE rows, scale operands) and finish() waits for
+// them and writes the query rows to `q_tile` ([local_head * T + t][D]), the K/V rows to this
+// step's k_new/v_new rows and, when the QKV arguments carry a cache, to the cache row
+// (p + t) % capacity. The kernel issues load() before its first K/V stages, so the in-order
+// memory counter lets finish() wait for these few loads alone.
+constexpr int kFusedQkvMaxTokens = 8;
+constexpr int kFusedQkvUnitsPerWave = 8;
+
+template <int D, int S>
+struct FusedQkv {
+  static constexpr int E = D / 64;
+  static constexpr int U = kFusedQkvUnitsPerWave;
+  static_assert(E == 2, "two elements per lane");
+  float part[U][S][E], wv[U][E], cs[U][E], sn[U][E];
+  float amax_part, w_scale;
+
+  __device__ __forceinline__ static uint32_t load_u32(const bf16_t *p) {
+    return *reinterpret_cast<const uint32_t *>(p);
+  }
+  __device__ __forceinline__ static void unpack(uint32_t w, float (&v)[E]) {
+    v[0] = __uint_as_float(w << 16);
+    v[1] = __uint_as_float(w & 0xffff0000u);
+  }
+
+  // unit u: query row (local head u / T, token u % T), then the T K rows, then the T V rows
+  __device__ __forceinline__ static void unit(int u, int G, int T, int &kind, int &t) {
+    kind = u < G * T ? 0 : 1 + (u - G * T) / T;
+    t = u < G * T ? u % T : (u - G * T) % T;
+  }
+
+  __device__ __forceinline__ void load(const AttentionArgs &a, int r, int h, int p) {
+    const QkvArgs &q = a.qkv;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
+    const int hq = a.query_heads, hkv = a.kv_heads, G = hq / hkv, T = a.tokens;
+    const int query_width = hq * D, kv_width = hkv * D;
+    const int packed_width = query_width + kv_width * (q.key_equals_value ? 1 : 2);
+    const int units = G * T + (q.key_equals_value ? 1 : 2) * T;
+    amax_part = amax_lane(q.x_amax, q.amax_stripes);
+    w_scale = *q.w_scale;
+    // Branch-free: past the last unit a wave re-loads the last one (its values are not used), so
+    // no control-flow merge makes the compiler wait for these loads before the K/V stages go out.
+#pragma unroll
+    for (int i = 0; i < U; ++i) {
+      const int u = min(wave + i * waves, units - 1);
+      int kind, t;
+      unit(u, G, T, kind, t);
+      const int column0 = kind == 0 ? (h * G + u / T) * D
+                          : kind == 1 ? query_width + h * D
+                                      : query_width + kv_width + h * D;
+      const int row = r * T + t;
+      const int c0 = column0 + lane * E;
+#pragma unroll
+      for (int k = 0; k < S; ++k) {
+        const float2 v = *reinterpret_cast<const float2 *>(
+            q.partials + (static_cast<size_t>(k) * q.rows + row) * packed_width + c0);
+        part[i][k][0] = v.x;
+        part[i][k][1] = v.y;
+      }
+      const size_t rope = static_cast<size_t>(p + t) * D + lane * E;
+      unpack(load_u32((kind == 1 ? q.k_norm : q.q_norm) + lane * E), wv[i]);
+      unpack(load_u32(q.cosine + rope), cs[i]);
+      unpack(load_u32(q.sine + rope), sn[i]);
+    }
+  }
+
+  __device__ __forceinline__ void finish(const AttentionArgs &a, int r, int h, int p, int slot,
+                                         bf16_t *q_tile) {
+    const QkvArgs &q = a.qkv;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
+    const int hq = a.query_heads, hkv = a.kv_heads, G = hq / hkv, T = a.tokens;
+    const int units = G * T + (q.key_equals_value ? 1 : 2) * T;
+    const float scale = w_scale * fp8_scale_from_amax(wave_max(amax_part));
+    // per unit: split-K sum, bf16, RMSNorm (Q, K with weight; V without), RoPE (Q, K). The
+    // arithmetic of every unit comes first, branch-free (both the rotated and the plain result),
+    // so the units' dependency chains interleave; past the last unit a wave redoes the last one.
+    uint32_t roped[U], plain[U];
+#pragma unroll
+    for (int i = 0; i < U; ++i) {
+      float x[E];
+      float square_sum = 0.0f;
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        float sum = part[i][0][e];
+#pragma unroll
+        for (int k = 1; k < S; ++k) sum += part[i][k][e];
+        x[e] = round_bf16(sum * scale);
+        square_sum += x[e] * x[e];
+      }
+      const float inv = inverse_rms(wave_sum(square_sum), D, q.eps);
+      float normalized[E], out[E];
+#pragma unroll
+      for (int e = 0; e < E; ++e) normalized[e] = round_bf16(x[e] * inv * wv[i][e]);
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        const int d = lane * E + e;
+        const float partner = __shfl_xor(normalized[e], 32, kWave);
+        const float rotated = d < D / 2 ? -partner : partner;
+        out[e] = normalized[e] * cs[i][e] + rotated * sn[i][e];
+      }
+      roped[i] = f32x2_to_bf16x2(out[0], out[1]);
+      plain[i] = f32x2_to_bf16x2(x[0] * inv, x[1] * inv);
+    }
+    // stores: Q rows to the tile, K (RoPE) and V (no weight; K = V: the K head's plain result)
+    // rows to this step's rows and the cache
+#pragma unroll
+    for (int i = 0; i < U; ++i) {
+      const int u = wave + i * waves;
+      if (u >= units) break;  // wave-uniform
+      int kind, t;
+      unit(u, G, T, kind, t);
+      const int row = r * T + t;
+      auto write_kv = [&](bf16_t *new_rows, bf16_t *cache, uint32_t vals) {
+        *reinterpret_cast<uint32_t *>(new_rows + (static_cast<size_t>(row) * hkv + h) * D + lane * E) = vals;
+        if (cache != nullptr)
+          *reinterpret_cast<uint32_t *>(
+              cache + ((static_cast<size_t>(slot) * hkv + h) * q.capacity + (p + t) % q.capacity) * D +
+              lane * E) = vals;
+      };
+      if (kind == 0)
+        *reinterpret_cast<uint32_t *>(q_tile + u * D + lane * E) = roped[i];
+      else if (kind == 1)
+        write_kv(q.k_new, q.k_cache, roped[i]);
+      if (kind == 2 || (kind == 1 && q.key_equals_value)) write_kv(q.v_new, q.v_cache, plain[i]);
+    }
+  }
+};
+
+// kFuseSplits > 0: the QKV post-processing of the step over that many split-K partials is fused
+// into the prologue (AttentionArgs::fuse_qkv).
+template <int D, int NQ, bool kFp8, AttentionMode kMode, int kWaves, int kFuseSplits = 0>
 __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(kAttentionOccupancy<D, NQ>)))
 void attention_kernel(const AttentionArgs a) {
   constexpr int kThreads = kWaves * 64;
@@ -124,7 +258,9 @@ void attention_kernel(const AttentionArgs a) {
   constexpr int kWaveBytes = kStages * kStageBytes;
   constexpr int kCombineBytes = (2 * kWaves * NQ * 16 + kWaves * NQ * 16 * D) * 4;
   constexpr int kLoopBytes = kWaves * kWaveBytes + kQBytes;  // V stages, then Q (kQInLds)
-  constexpr int kLdsBytes = kLoopBytes > kCombineBytes ? kLoopBytes : kCombineBytes;
+  // the fused QKV post-processing's query rows [16][D] bf16 sit past the stages
+  constexpr int kQTileBytes = kFuseSplits > 0 ? 16 * D * 2 : 0;
+  constexpr int kLdsBytes = (kLoopBytes > kCombineBytes ? kLoopBytes : kCombineBytes) + kQTileBytes;
   static_assert(KPI % kRowsPerDma == 0 && kRowsPerDma * kChunksPerRow == 64, "DMA row tiling");
   __shared__ __attribute__((aligned(16))) unsigned char lds[kLdsBytes];
 
@@ -199,7 +335,8 @@ void attention_kernel(const AttentionArgs a) {
     return fresh ? new_head + (key - p) * a.kv_heads : cache_head + physical;
   };
   auto issue = [&](int it, int st) {
-    const int kbase = first + min(it, iterations - 1) * stride;
+    // (a wave without iterations re-reads a valid row of the chunk; its loads are never used)
+    const int kbase = first + max(0, min(it, iterations - 1)) * stride;
     unsigned char *vst = wave_lds + st * kStageBytes;
 #pragma unroll
     for (int j = 0; j < kDmaPerTensor; ++j) {
@@ -231,9 +368,32 @@ void attention_kernel(const AttentionArgs a) {
   // round trips overlap.
   // With a single stage, iteration 0's loads go out here and each later one after the previous
   // iteration's compute.
-  if (iterations > 0) {
+  constexpr int kEarlyStages = kStages > 1 ? kStages - 1 : 1;
+  auto issue_early = [&] {
+    if (iterations > 0) {
 #pragma unroll
-    for (int st = 0; st < (kStages > 1 ? kStages - 1 : 1); ++st) issue(st, st);
+      for (int st = 0; st < kEarlyStages; ++st) issue(st, st);
+    }
+  };
+  // With the QKV post-processing fused, this step's K/V rows are written by the workgroup itself
+  // first, and only stages issued after those stores may read them (key >= p).
+  constexpr bool kFuseQkv = kFuseSplits > 0;
+  FusedQkv<(kFuseSplits > 0 ? D : 128), (kFuseSplits > 0 ? kFuseSplits : 1)> fused;
+  // Fused QKV: every wave's loads of stages 0 .. 2 kStages - 3 (the early ones and those issued
+  // in loop iterations 0 .. kStages - 2) stay below p when the range starts 2 kStages - 2
+  // strides before it; the K/V rows' stores then need no wait of their own: a wave's in-order
+  // memory counter has retired them once iteration kStages - 2 waited for its stage, and the
+  // workgroup barrier at iteration kStages - 1 makes that so for every wave before any fresh key
+  // is loaded. For shorter ranges the early stages are issued again after the stores.
+  const bool kv_async = kFuseQkv && chunk_lo + (2 * kStages - 2) * stride <= p;
+  if constexpr (kFuseQkv) {
+    // The prologue's loads go out before the stages (so that waiting for them does not wait for
+    // the stages), and the stages unconditionally: a branch here would merge into a full wait.
+    fused.load(a, r, h, p);
+#pragma unroll
+    for (int st = 0; st < kEarlyStages; ++st) issue(st, st);
+  } else {
+    issue_early();
   }
 
   // ---- Q operands: column = query row, K-group = d slice. Query row qr = local_head * T + t.
@@ -243,6 +403,27 @@ void attention_kernel(const AttentionArgs a) {
   u32x4 qop[NQ][kQRegSteps];
   u32x4 *q_lds = reinterpret_cast<u32x4 *>(lds + kWaves * kWaveBytes);
   int row_t[NQ];
+  if constexpr (kFuseQkv) {
+    static_assert(NQ == 1 && !kQInLds && !kFp8 && kMode != AttentionMode::decode, "fused QKV shape");
+    // the query rows [qr = local_head * T + t][D] bf16, in LDS of their own
+    bf16_t *q_tile = reinterpret_cast<bf16_t *>(lds + kLdsBytes - kQTileBytes);
+    fused.finish(a, r, h, p, slot, q_tile);
+    if (kv_async) {
+      wait_lgkmcnt0();  // the query rows are in LDS (the K/V stores stay in flight)
+      __builtin_amdgcn_s_barrier();
+    } else {
+      wait_vmcnt<0>();  // this step's K/V rows are stored (and the early stages have landed)
+      __syncthreads();
+      issue_early();    // again: they may have read fresh rows before the stores
+    }
+    const int qr = col;
+    const bool valid = qr < qrows;
+    row_t[0] = valid ? qr % T : -1;
+#pragma unroll
+    for (int s = 0; s < DS; ++s)
+      qop[0][s] = valid ? *reinterpret_cast<const u32x4 *>(q_tile + qr * D + s * 32 + group * 8)
+                        : u32x4{0u, 0u, 0u, 0u};
+  } else {
 #pragma unroll
   for (int nq = 0; nq < NQ; ++nq) {
     const int qr = q0 + nq * 16 + col;
@@ -262,6 +443,7 @@ void attention_kernel(const AttentionArgs a) {
         qop[nq][s] = valid ? *reinterpret_cast<const u32x4 *>(qrow + s * 32 + group * 8)
                            : u32x4{0u, 0u, 0u, 0u};
     }
+  }
   }
   if constexpr (kQInLds) __syncthreads();
   auto q_operand = [&](int nq, int s) -> u32x4 {
@@ -432,6 +614,8 @@ void attention_kernel(const AttentionArgs a) {
       for (int j = 0; j < kStages; ++j) {
         const int it = it0 + j;
         if (it >= iterations) break;
+        // fused QKV: every wave's K/V row stores have retired (see kv_async)
+        if (kFuseQkv && kv_async && it == kStages - 1) __builtin_amdgcn_s_barrier();
         __asm__ volatile("" ::: "memory");  // the previous iteration's LDS reads stay above
         if constexpr (kStages > 1) issue(it + kStages - 1, (j + kStages - 1) % kStages);
         wait_vmcnt<(kStages - 1) * kLoadsPerStage>();
@@ -443,8 +627,8 @@ void attention_kernel(const AttentionArgs a) {
         }
       }
     }
-    wait_vmcnt<0>();  // the clamped tail DMAs must land before the LDS is reused below
   }
+  wait_vmcnt<0>();  // the clamped tail DMAs must land before the LDS is reused below
 
   // ---- combine the waves through LDS: per wave m, l (per query row) and O rows.
   __syncthreads();
@@ -954,9 +1138,30 @@ void launch_mode(const AttentionArgs &a, dim3 grid, hipStream_t stream) {
   }
 }
 
+// Verify attention with the step's QKV post-processing fused (attention_can_fuse_qkv).
+template <int S>
+void launch_fused(const AttentionArgs &a, dim3 grid, hipStream_t stream) {
+  if (a.mode == AttentionMode::sliding)
+    attention_kernel<128, 1, false, AttentionMode::sliding, kAttentionWaves, S>
+        <<<grid, kAttentionWaves * 64, 0, stream>>>(a);
+  else
+    attention_kernel<128, 1, false, AttentionMode::global, kAttentionWaves, S>
+        <<<grid, kAttentionWaves * 64, 0, stream>>>(a);
+}
+
 template <int D, int NQ>
 void launch_typed(const AttentionArgs &a, dim3 grid, hipStream_t stream) {
   if (a.timing_start != nullptr) hip_check(hipEventRecord(a.timing_start, stream), "record probe");
+  if constexpr (D == 128 && NQ == 1) {
+    if (a.fuse_qkv) {
+      if (a.qkv.splits == 1)
+        launch_fused<1>(a, grid, stream);
+      else
+        launch_fused<2>(a, grid, stream);
+      if (a.timing_stop != nullptr) hip_check(hipEventRecord(a.timing_stop, stream), "record probe");
+      return;
+    }
+  }
   if (a.fp8_kv)
     launch_mode<D, NQ, true>(a, grid, stream);
   else
@@ -974,6 +1179,22 @@ void launch_typed(const AttentionArgs &a, dim3 grid, hipStream_t stream) {
 }
 
 }  // namespace
+
+bool attention_can_fuse_qkv(const AttentionArgs &a) {
+  const QkvArgs &q = a.qkv;
+  const int G = a.kv_heads > 0 ? a.query_heads / a.kv_heads : 0;
+  const int units = G * a.tokens + (q.key_equals_value ? 1 : 2) * a.tokens;
+  return (a.mode == AttentionMode::sliding || a.mode == AttentionMode::global) && a.dimension == 128 &&
+         !a.fp8_kv && G > 0 && G * a.tokens <= 16 && a.tokens <= kFusedQkvMaxTokens &&
+         units <= kAttentionWaves * kFusedQkvUnitsPerWave && a.chunk_keys > 0 &&
+         (a.max_keys + a.chunk_keys - 1) / a.chunk_keys == 1 && q.partials != nullptr &&
+         (q.splits == 1 || q.splits == 2) && q.x_amax != nullptr && q.w_scale != nullptr &&
+         q.rows == a.requests * a.tokens && q.tokens == a.tokens && q.query_heads == a.query_heads &&
+         q.kv_heads == a.kv_heads && q.dimension == 128 && q.q_norm != nullptr &&
+         q.k_norm != nullptr && q.cosine != nullptr && q.sine != nullptr && q.positions == a.positions &&
+         q.slots == a.slots && q.position_offset == 0 && q.k_new == a.k_new && q.v_new == a.v_new &&
+         (q.k_cache == nullptr || (q.v_cache != nullptr && q.capacity > 0));
+}
 
 size_t attention_partials_floats(int requests, int kv_heads, int max_keys, int chunk_keys,
                                  int query_rows, int dimension) {
@@ -1024,6 +1245,9 @@ void launch_attention(const AttentionArgs &a, hipStream_t stream) {
     throw std::runtime_error("sliding attention window must fit the ring");
   if (a.mode == AttentionMode::decode && a.tokens != 1)
     throw std::runtime_error("decode attention takes one query token");
+  if (a.fuse_qkv && !attention_can_fuse_qkv(a))
+    throw std::runtime_error("this attention call cannot take the QKV post-processing");
+  if (a.fuse_qkv) check_amax_stripes(a.qkv.amax_stripes);
   const int qrows = (a.query_heads / a.kv_heads) * a.tokens;
   const int max_chunks = (a.max_keys + a.chunk_keys - 1) / a.chunk_keys;
   if (max_chunks > 1 && a.partials == nullptr)

@@ -608,6 +608,9 @@ int carat_hip_runner_set_graphs(carat_hip_runner *runner, int enabled) {
   return guarded([&] { runner_of(runner).set_graphs_enabled(enabled != 0); });
 }
 
+int carat_hip_runner_set_qkv_fusion(carat_hip_runner *runner, int enabled) {
+  return guarded([&] { runner_of(runner).set_qkv_fusion(enabled != 0); });
+}
 int carat_hip_runner_set_fused_quantization(carat_hip_runner *runner, int enabled) {
   return guarded([&] { runner_of(runner).set_fused_quantization(enabled); });
 }

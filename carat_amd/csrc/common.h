@@ -126,6 +126,11 @@ __device__ __forceinline__ float wave_max(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
+// RMSNorm's 1 / sqrt(mean square + eps) (cuda/ops.cu:27-85).
+__device__ __forceinline__ float inverse_rms(float square_sum, int width, float eps) {
+  return rsqrtf(square_sum / static_cast<float>(width) + eps);
+}
+
 // Block-wide sum; `scratch` needs blockDim.x / 64 floats. All threads get the result.
 __device__ __forceinline__ float block_sum(float v, float *scratch) {
   v = wave_sum(v);

@@ -14,10 +14,6 @@ constexpr int kQkvUnrolledSplits = 4;  // split-K partials the QKV post-processi
 constexpr int kMaxAcceptRows = 1024;    // rows per request of a forced (prefill) commit
 constexpr int kRowMaxQuadsPerThread = 4;  // widths up to 16384
 
-__device__ __forceinline__ float inverse_rms(float square_sum, int width, float eps) {
-  return rsqrtf(square_sum / static_cast<float>(width) + eps);
-}
-
 __device__ __forceinline__ f32x4_t bf16x4_to_f32(uint2 v) {
   return f32x4_t{__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xffff0000u),
                  __uint_as_float(v.y << 16), __uint_as_float(v.y & 0xffff0000u)};

@@ -172,6 +172,9 @@ public:
   // with a zero bound on the workgroups' wait for the agreed amax, so that every waiting
   // workgroup reports a timeout and the step raises (a test of that error path).
   void set_fused_quantization(int mode);
+  // Whether verify attention post-processes its own QKV rows (true, the default: one launch fewer
+  // per layer) or the separate QKV kernel runs first; the results are the same bit for bit.
+  void set_qkv_fusion(bool enabled);
   // Milliseconds of the last verify / draft call's device work (hip events on the runner stream).
   float last_verify_ms() const;
   float last_draft_ms() const;

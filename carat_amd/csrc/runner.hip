@@ -224,6 +224,8 @@ struct BatchModelRunner::Implementation {
   // 0 (default): separate prepare kernels, measured faster in the step than the fused
   // quantisation (1); 2: fused with a zero wait bound (error-path test)
   int fused_quantize_mode = 0;
+  // verify attention post-processes the QKV rows itself where it can (attention_can_fuse_qkv)
+  bool qkv_fusion = true;
   bool last_input_prepared = false;
   size_t io_ints = 0;
   int sliding_layer_count = 0;
@@ -306,6 +308,12 @@ struct BatchModelRunner::Implementation {
       ++probe_launches;
     }
     probe_used = 0;
+  }
+
+  void set_qkv_fusion(bool enabled) {
+    qkv_fusion = enabled;
+    for (auto &entry : verify_graphs) (void)hipGraphExecDestroy(entry.second);
+    verify_graphs.clear();  // captured steps hold the previous choice
   }
 
   void set_fused_quantization(int mode) {
@@ -1053,8 +1061,12 @@ struct BatchModelRunner::Implementation {
       q.v_cache = L.v_cache.as<bf16_t>();
       q.capacity = L.capacity;
     }
-    launch_qkv_post(q, stream);
     AttentionArgs at = layer_attention(li, io.requests, io.depth, io.positions, io.slots);
+    // The attention kernel post-processes its own (request, kv head)'s QKV rows where it can
+    // (same arithmetic, one launch fewer per layer); otherwise the separate kernel runs first.
+    at.qkv = q;
+    at.fuse_qkv = qkv_fusion && attention_can_fuse_qkv(at);
+    if (!at.fuse_qkv) launch_qkv_post(q, stream);
     std::tie(at.timing_start, at.timing_stop) =
         probe(L.spec.sliding ? probe_sliding_attention : probe_global_attention);
     launch_attention(at, stream);
@@ -2224,6 +2236,7 @@ void *BatchModelRunner::tensor(const std::string &name, size_t *bytes,
 }
 hipStream_t BatchModelRunner::stream() const { return implementation_->stream; }
 void BatchModelRunner::set_graphs_enabled(bool enabled) { implementation_->graphs_enabled = enabled; }
+void BatchModelRunner::set_qkv_fusion(bool enabled) { implementation_->set_qkv_fusion(enabled); }
 void BatchModelRunner::set_fused_quantization(int mode) {
   implementation_->set_fused_quantization(mode);
 }

@@ -320,6 +320,11 @@ class BatchModelRunner:
     def set_graphs(self, enabled: bool) -> None:
         check(lib().carat_hip_runner_set_graphs(self._handle, int(enabled)))
 
+    def set_qkv_fusion(self, enabled: bool) -> None:
+        """Whether verify attention post-processes its own QKV rows (default) or the separate
+        QKV kernel runs first; the same results bit for bit."""
+        check(lib().carat_hip_runner_set_qkv_fusion(self._handle, int(enabled)))
+
     def set_fused_quantization(self, mode: int) -> None:
         """0 (default) separate quantisation kernel, 1 fused into the layer-end rows, 2 fused with a
         zero wait bound (error-path test)."""

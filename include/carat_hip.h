@@ -216,6 +216,10 @@ int carat_hip_runner_set_graphs(carat_hip_runner *runner, int enabled);
  * on the workgroups' wait for the agreed amax, so the step reports the timeout error (a test of
  * that path). Other values are rejected. */
 int carat_hip_runner_set_fused_quantization(carat_hip_runner *runner, int enabled);
+/* No reference counterpart: 1 (default) lets the verify attention kernel post-process its own
+ * (request, kv head)'s QKV rows (Q/K norm, RoPE, this step's K/V rows) where the shape allows,
+ * one launch fewer per layer; 0 runs the separate QKV kernel first. Same results bit for bit. */
+int carat_hip_runner_set_qkv_fusion(carat_hip_runner *runner, int enabled);
 int carat_hip_runner_timing(carat_hip_runner *runner, float *verify_ms, float *draft_ms);
 /* Benchmark helper, no counterpart in the reference: one speculative cycle of the reference's
  * scheduler (native_runtime_main.cpp:583-678) in C++ -- draft_four(last, slots, forced, depth),

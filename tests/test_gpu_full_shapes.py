@@ -349,6 +349,32 @@ def test_config5_fused_quantization_equals_the_separate_kernel(full_model):
         assert np.array_equal(a, b), name
 
 
+def test_config5_qkv_fusion_equals_the_separate_kernel(full_model):
+    """At config-5 dimensions (two split-K partials, 24 x 16 attention workgroups, each
+    post-processing its own rows) the fused step equals the separate QKV kernel's bit for bit:
+    predictions, final hidden rows, this step's K/V rows and the global layer's cache."""
+    desc, runner, positions_by_slot = full_model
+    rng = np.random.default_rng(59)
+    slots = rng.permutation(SLOTS).astype(np.int32)
+    props = rng.integers(0, VOCAB, (SLOTS, T)).astype(np.int32)
+    first = props[:, 0].copy()
+    names = ["final_hidden"] + [f"new.{li}.{kind}" for li in range(len(desc.layers)) for kind in ("k", "v")]
+    names += [f"cache.{li}.{kind}" for li, l in enumerate(desc.layers) if not l.sliding for kind in ("k", "v")]
+    out = []
+    for fused in (True, False):
+        say(f"case: config-5 dry verify, QKV fusion {fused}")
+        runner.set_qkv_fusion(fused)
+        try:
+            res = runner.verify_greedy_proposals(props.tolist(), first.tolist(), slots.tolist(), [0] * SLOTS)
+            assert res.accepted_tokens == [0] * SLOTS
+            out.append((list(runner.last_predictions), [runner.read(n, np.uint16).copy() for n in names]))
+        finally:
+            runner.set_qkv_fusion(True)
+    assert out[0][0] == out[1][0]
+    for name, a, b in zip(names, out[0][1], out[1][1]):
+        assert np.array_equal(a, b), name
+
+
 def test_config5_draft_step_full_dimensions(full_model):
     """A forced step and one free step of the full-size assistant (hidden 1024, 4 layers, bf16)
     over the 24 slots' caches, against the oracle chain teacher-forced on the GPU's tokens."""

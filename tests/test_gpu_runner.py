@@ -203,6 +203,38 @@ def test_fused_quantization_equals_the_separate_kernel(model):
         assert np.array_equal(a, b), name
 
 
+def qkv_fusion_on_and_off(runner, props, first, slots, names):
+    """One dry verify with the QKV post-processing inside the attention kernel, one with the
+    separate kernel: predictions and the named tensors of both."""
+    out = []
+    for fused in (True, False):
+        runner.set_qkv_fusion(fused)
+        try:
+            runner.verify_greedy_proposals(props, first, slots, [0] * len(slots))
+            out.append((list(runner.last_predictions), [runner.read(n, np.uint16).copy() for n in names]))
+        finally:
+            runner.set_qkv_fusion(True)
+    return out
+
+
+def test_qkv_fusion_equals_the_separate_kernel(model):
+    """Verify attention post-processes its own (request, kv head)'s QKV rows (split-K sum, Q/K
+    norm, RoPE, V norm) with the QKV kernel's arithmetic: predictions, final hidden rows, this
+    step's K/V rows and the global layer's cache rows equal the separate kernel's bit for bit."""
+    desc, runner = model
+    reset_state(runner, [40, 55, 70, 90], seed=15)
+    rng = np.random.default_rng(23)
+    props = rng.integers(0, desc.vocabulary, (4, 5)).tolist()
+    first = [p[0] for p in props]
+    say("case: fused vs separate QKV post-processing, tiny model")
+    names = ["final_hidden"] + [f"new.{li}.{kind}" for li in range(len(desc.layers)) for kind in ("k", "v")]
+    names += [f"cache.{li}.{kind}" for li, l in enumerate(desc.layers) if not l.sliding for kind in ("k", "v")]
+    (p_fused, t_fused), (p_sep, t_sep) = qkv_fusion_on_and_off(runner, props, first, [2, 0, 3, 1], names)
+    assert p_fused == p_sep
+    for name, a, b in zip(names, t_fused, t_sep):
+        assert np.array_equal(a, b), name
+
+
 def test_fused_quantization_wait_timeout_is_an_error(model):
     """A layer-end workgroup whose wait for the agreed amax runs out sets a fault flag; the step
     raises instead of returning results from a partly quantised operand. Forced from the host with
