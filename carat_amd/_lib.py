@@ -33,6 +33,7 @@ EXPORTED = [
     "carat_hip_runner_timing", "carat_hip_runner_set_probe", "carat_hip_runner_read_probe",
     "carat_hip_runner_stream_gemm_probe", "carat_hip_bench_speculative_cycle",
     "carat_hip_argmax_accept", "carat_hip_argmax_accept_noalloc", "carat_hip_gemm_plan", "carat_hip_fp8_linear",
+    "carat_hip_fp8_linear_scaled", "carat_hip_fp8_weight_scale_elements", "carat_hip_quantize_weight_fp8",
     "carat_hip_bf16_linear", "carat_hip_verify_attention", "carat_hip_row_op",
     "carat_hip_qkv_post", "carat_hip_rope_table", "carat_hip_f32_to_e4m3",
 ]
@@ -49,7 +50,7 @@ class ModelDesc(ctypes.Structure):
                 ("layers", POINTER(LayerDesc)), ("assistant", c_int), ("assistant_hidden", c_int),
                 ("assistant_intermediate", c_int), ("assistant_layers", c_int),
                 ("assistant_query_heads", c_int), ("seed", c_uint64), ("weight_std", c_float),
-                ("assistant_fp8_mode", c_int)]
+                ("assistant_fp8_mode", c_int), ("fp8_scaling", c_int)]
 
 
 class RowArgs(ctypes.Structure):

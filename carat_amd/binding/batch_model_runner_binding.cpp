@@ -53,10 +53,10 @@ Gemma4BatchModelRunner::Gemma4BatchModelRunner(const Gemma4Config &config,
                                                const Fp8WeightArena *fp8_weights,
                                                const DeviceWeightArena *assistant_weights,
                                                const Fp8WeightArena *assistant_fp8_weights) {
-  // The runner's projections are per-tensor e4m3; an arena quantised another way cannot be used.
-  for (const Fp8WeightArena *arena : {fp8_weights, assistant_fp8_weights})
-    if (arena != nullptr && arena->scaling() != Fp8Scaling::tensor)
-      throw std::runtime_error("MI355X runner serves per-tensor FP8 weights only");
+  // The target arena may be quantised per tensor, channel or 128 x 128 block; the assistant's
+  // Fp8Linear is per tensor (assistant_runner.cu:123-125), so its arena must be too.
+  if (assistant_fp8_weights != nullptr && assistant_fp8_weights->scaling() != Fp8Scaling::tensor)
+    throw std::runtime_error("assistant FP8 weights must be quantized per tensor");
   std::vector<carat_hip_layer_desc> layers;
   layers.reserve(config.layers.size());
   for (const Gemma4LayerConfig &layer : config.layers)
@@ -81,6 +81,10 @@ Gemma4BatchModelRunner::Gemma4BatchModelRunner(const Gemma4Config &config,
   // assistant runner (assistant_runner.cu:31-44); lm_head and all read the assistant FP8 arena
   // and fail without it.
   desc.assistant_fp8_mode = 0;
+  desc.fp8_scaling = fp8_weights == nullptr ? 0
+                     : fp8_weights->scaling() == Fp8Scaling::channel ? 1
+                     : fp8_weights->scaling() == Fp8Scaling::block_128 ? 2
+                                                                     : 0;
   ArenaSet arenas{{&weights, assistant_weights}, {fp8_weights, assistant_fp8_weights}};
   hip_ok(carat_hip_runner_create_from_device_weights(&desc, arena_segment, &arenas, batch,
                                                      maximum_context, &runner_));

@@ -55,6 +55,8 @@ struct OpWorkspace {
   size_t packed_weight_bytes = 0;
   void *amax = nullptr;           // striped amax of a split attention call
   size_t amax_bytes = 0;
+  void *x_scales = nullptr;       // activation scales of a channel / block_128 linear
+  size_t x_scale_bytes = 0;
 };
 constexpr int kOpAmaxStripes = 64;
 std::mutex workspace_mutex;
@@ -101,6 +103,9 @@ ModelSpec spec_from_desc(const carat_hip_model_desc *d) {
   if (d->assistant_fp8_mode < 0 || d->assistant_fp8_mode > 3)
     throw std::runtime_error("assistant_fp8_mode must be 0 (environment), 1 off, 2 lm_head or 3 all");
   spec.assistant.fp8_mode = d->assistant_fp8_mode - 1;
+  if (d->fp8_scaling < 0 || d->fp8_scaling > 2)
+    throw std::runtime_error("fp8_scaling must be 0 tensor, 1 channel or 2 block_128");
+  spec.fp8_scaling = d->fp8_scaling;
   spec.seed = d->seed;
   spec.weight_std = d->weight_std;
   return spec;
@@ -193,6 +198,7 @@ int carat_hip_gemma4_benchmark_desc(carat_hip_model_desc *desc, carat_hip_layer_
     desc->assistant_query_heads = spec.assistant.query_heads;
     desc->seed = spec.seed;
     desc->weight_std = spec.weight_std;
+    desc->fp8_scaling = spec.fp8_scaling;
   });
 }
 
@@ -729,9 +735,10 @@ int carat_hip_argmax_accept_noalloc(const float *logits_f32, const uint16_t *log
 static int linear_common(bool fp8, const uint16_t *x, int m, int k, const float *x_amax,
                          const void *w, int n, const float *w_scale, int epilogue, int splits,
                          uint16_t *y, float *y_amax, float *partial, int32_t *predictions,
-                         void *stream) {
+                         void *stream, int scaling = 0) {
   return guarded([&] {
     if (epilogue < 0 || epilogue > 3) throw std::runtime_error("invalid GEMM epilogue");
+    if (scaling < 0 || scaling > 2) throw std::runtime_error("fp8_scaling must be 0, 1 or 2");
     GemmArgs g;
     g.x = x;
     g.ldx = k;
@@ -757,6 +764,17 @@ static int linear_common(bool fp8, const uint16_t *x, int m, int k, const float 
       ensure(ws.xprep, ws.xprep_bytes, gemm_xprep_bytes(m, k), "allocate GEMM activation workspace");
       g.xprep = static_cast<unsigned char *>(ws.xprep);
       g.xprep_capacity = ws.xprep_bytes;
+    }
+    if (scaling != 0) {
+      if (w_scale == nullptr) throw std::runtime_error("scaled FP8 linear needs weight scales");
+      ensure(ws.x_scales, ws.x_scale_bytes, sizeof(float) * gemm_x_scale_floats(m, k),
+             "allocate activation scale workspace");
+      g.scaling = scaling;
+      g.w_scales = w_scale;
+      g.w_scale_kblocks = static_cast<int>(fp8_weight_scale_elements(2, n, k) / ((n + 127) / 128));
+      g.x_scales = static_cast<float *>(ws.x_scales);
+      g.x_scales_capacity = ws.x_scale_bytes / sizeof(float);
+      g.w_scale = nullptr;
     }
     g.w_layout = gemm_weight_layout(n, k * (fp8 ? 1 : 2), g.epilogue == GemmEpilogue::gelu_gate);
     ensure(ws.packed_weight, ws.packed_weight_bytes,
@@ -793,6 +811,35 @@ int carat_hip_fp8_linear(const uint16_t *x, int m, int k, const float *x_amax, c
                          float *y_amax, float *partial, int32_t *predictions, void *stream) {
   return linear_common(true, x, m, k, x_amax, w, n, w_scale, epilogue, splits, y, y_amax, partial,
                        predictions, stream);
+}
+
+int carat_hip_fp8_linear_scaled(const uint16_t *x, int m, int k, int fp8_scaling, const uint8_t *w,
+                                int n, const float *w_scales, int epilogue, int splits, uint16_t *y,
+                                float *partial, int32_t *predictions, void *stream) {
+  if (fp8_scaling != 1 && fp8_scaling != 2)
+    return guarded([] { throw std::runtime_error("fp8_scaling must be 1 (channel) or 2 (block_128)"); });
+  return linear_common(true, x, m, k, nullptr, w, n, w_scales, epilogue, splits, y, nullptr, partial,
+                       predictions, stream, fp8_scaling);
+}
+
+int carat_hip_fp8_weight_scale_elements(int fp8_scaling, int n, int k, uint64_t *out) {
+  return guarded([&] {
+    if (out == nullptr || n <= 0 || k <= 0) throw std::runtime_error("invalid FP8 weight shape");
+    *out = fp8_weight_scale_elements(fp8_scaling, n, k);
+  });
+}
+
+int carat_hip_quantize_weight_fp8(const uint16_t *w, int n, int k, int fp8_scaling, uint8_t *out,
+                                  float *scales, void *stream) {
+  return guarded([&] {
+    if (w == nullptr || out == nullptr || scales == nullptr)
+      throw std::runtime_error("invalid FP8 weight quantization arguments");
+    std::lock_guard<std::mutex> lock(workspace_mutex);
+    OpWorkspace &ws = workspace_for_current_device();
+    ensure(ws.amax, ws.amax_bytes, sizeof(float) * kOpAmaxStripes * 64, "allocate amax workspace");
+    quantize_weight_bf16_to_fp8_scaled(w, reinterpret_cast<fp8_t *>(out), n, k, fp8_scaling, scales,
+                                       static_cast<float *>(ws.amax), static_cast<hipStream_t>(stream));
+  });
 }
 
 int carat_hip_bf16_linear(const uint16_t *x, int m, int k, const uint16_t *w, int n, int epilogue,

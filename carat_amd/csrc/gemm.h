@@ -52,6 +52,16 @@ struct GemmArgs {
   int n = 0;
   WeightLayout w_layout;           // must describe w (n, row bytes, F, gate/up)
   const float *w_scale = nullptr;  // fp8 only: per-tensor weight scale (device)
+  // Fp8Scaling (include/carat/linear.h:27): 0 tensor (x_amax, w_scale); 1 channel and
+  // 2 block_128 quantise the activations per token row / per token and 128-element K block
+  // themselves and scale inside the GEMM, every epilogue's output carrying the full scale:
+  // w_scales [n] (channel) or [ceil(n/128)][w_scale_kblocks] (block_128, Fp8WeightArena layout);
+  // x_scales a workspace of x_scales_capacity floats (gemm_x_scale_floats).
+  int scaling = 0;
+  const float *w_scales = nullptr;
+  int w_scale_kblocks = 0;
+  float *x_scales = nullptr;
+  size_t x_scales_capacity = 0;
   int k_splits = 1;
   GemmEpilogue epilogue = GemmEpilogue::store_bf16;
   bf16_t *y = nullptr;             // store_bf16 / gelu_gate output
@@ -78,6 +88,8 @@ struct GemmArgs {
 
 // Bytes of the e4m3 activation operand workspace for m rows of k elements.
 size_t gemm_xprep_bytes(int m, int k);
+// Floats of the activation scale workspace of a scaled (channel / block_128) e4m3 GEMM.
+size_t gemm_x_scale_floats(int m, int k);
 // 16-token tiles per token block of the e4m3 activation operand for m rows (2 or 8).
 inline int gemm_token_tiles(int m) { return m <= 32 ? 2 : 8; }
 // Keys of the argmax partial workspace for an m-row lm_head of this layout.

@@ -149,6 +149,96 @@ __global__ __launch_bounds__(256) void prepare_x_kernel(const bf16_t *x, int ldx
   reinterpret_cast<u32x4 *>(out)[static_cast<size_t>(m_block) * chunks_per_block + chunk] = value;
 }
 
+// Fp8Scaling::channel / ::block_128 activation operands (quantize_bf16_rows_kernel and
+// quantize_activation_block_128_kernel, cuda/linear.cu:300-316, 382-401): scale =
+// max(amax / 448, 2^-24) per token row (channel) or per token and 128-element K step (block_128),
+// q = e4m3(x / scale), written in the operand layout of prepare_x_kernel. Scales: channel
+// x_scales[token]; block_128 x_scales[m_block][step][col][token tile] (token = tile * 16 + col of
+// the block), so that a lane's token tiles of one step are contiguous. Tokens past m get zeros.
+__device__ __forceinline__ u32x4 quantize_chunk(u32x4 lo, u32x4 hi, float scale, bool live) {
+  u32x4 value = {0u, 0u, 0u, 0u};
+  if (!live) return value;
+  const uint32_t w[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+    value[q] = f32x4_to_e4m3x4(__uint_as_float(w[2 * q] << 16) / scale,
+                               __uint_as_float(w[2 * q] & 0xffff0000u) / scale,
+                               __uint_as_float(w[2 * q + 1] << 16) / scale,
+                               __uint_as_float(w[2 * q + 1] & 0xffff0000u) / scale);
+  return value;
+}
+
+__device__ __forceinline__ float chunk_amax(u32x4 lo, u32x4 hi) {
+  const uint32_t w[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+  float m = 0.0f;
+#pragma unroll
+  for (int q = 0; q < 8; ++q)
+    m = fmaxf(m, fmaxf(fabsf(__uint_as_float(w[q] << 16)), fabsf(__uint_as_float(w[q] & 0xffff0000u))));
+  return m;
+}
+
+// channel: one workgroup per token of the padded token blocks
+__global__ __launch_bounds__(256) void prepare_x_rows_kernel(const bf16_t *x, int ldx, int m, int k,
+                                                             int token_tiles, unsigned char *out,
+                                                             float *x_scales) {
+  const int token = blockIdx.x;
+  const int steps = k / kStepBytes;
+  const int m_block = token / (token_tiles * 16);
+  const int tile = (token / 16) % token_tiles;
+  const int col = token % 16;
+  const bool live = token < m;
+  const bf16_t *src = x + static_cast<size_t>(min(token, m - 1)) * ldx;
+  const int chunks = k / 16;
+  float amax = 0.0f;
+  for (int c = threadIdx.x; c < chunks; c += 256)
+    amax = fmaxf(amax, chunk_amax(*reinterpret_cast<const u32x4 *>(src + c * 16),
+                                  *reinterpret_cast<const u32x4 *>(src + c * 16 + 8)));
+  __shared__ float wave_maxima[4];
+  amax = wave_max(amax);
+  if ((threadIdx.x & 63) == 0) wave_maxima[threadIdx.x >> 6] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(wave_maxima[0], wave_maxima[1]), fmaxf(wave_maxima[2], wave_maxima[3]));
+  const float scale = fmaxf(amax / 448.0f, 0x1p-24f);
+  if (threadIdx.x == 0) x_scales[token] = scale;
+  for (int c = threadIdx.x; c < chunks; c += 256) {
+    const int step = c / 8, half = (c / 4) % 2, group = c % 4;
+    const u32x4 value = quantize_chunk(*reinterpret_cast<const u32x4 *>(src + c * 16),
+                                       *reinterpret_cast<const u32x4 *>(src + c * 16 + 8), scale, live);
+    const size_t chunk = ((static_cast<size_t>(m_block) * steps + step) * token_tiles + tile) * 128 +
+                         half * 64 + group * 16 + col;
+    reinterpret_cast<u32x4 *>(out)[chunk] = value;
+  }
+}
+
+// block_128: one wave per (token block, step, token tile); lane (group, col) holds both halves
+__global__ __launch_bounds__(256) void prepare_x_blocks_kernel(const bf16_t *x, int ldx, int m, int k,
+                                                               int token_tiles, unsigned char *out,
+                                                               float *x_scales) {
+  const int steps = k / kStepBytes;
+  const int w = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (w >= steps * token_tiles) return;  // wave-uniform
+  const int m_block = blockIdx.y;
+  const int step = w / token_tiles, tile = w % token_tiles;
+  const int lane = threadIdx.x & 63, group = lane >> 4, col = lane & 15;
+  const int token = m_block * token_tiles * 16 + tile * 16 + col;
+  const bf16_t *src = x + static_cast<size_t>(min(token, m - 1)) * ldx + step * 128 + group * 16;
+  const u32x4 lo0 = *reinterpret_cast<const u32x4 *>(src);
+  const u32x4 hi0 = *reinterpret_cast<const u32x4 *>(src + 8);
+  const u32x4 lo1 = *reinterpret_cast<const u32x4 *>(src + 64);
+  const u32x4 hi1 = *reinterpret_cast<const u32x4 *>(src + 72);
+  float amax = fmaxf(chunk_amax(lo0, hi0), chunk_amax(lo1, hi1));
+  amax = fmaxf(amax, __shfl_xor(amax, 16, kWave));
+  amax = fmaxf(amax, __shfl_xor(amax, 32, kWave));
+  const float scale = fmaxf(amax / 448.0f, 0x1p-24f);
+  const bool live = token < m;
+  u32x4 *dst = reinterpret_cast<u32x4 *>(out) +
+               ((static_cast<size_t>(m_block) * steps + step) * token_tiles + tile) * 128 + lane;
+  dst[0] = quantize_chunk(lo0, hi0, scale, live);
+  dst[64] = quantize_chunk(lo1, hi1, scale, live);
+  if (group == 0)
+    x_scales[((static_cast<size_t>(m_block) * steps + step) * 16 + col) * token_tiles + tile] = scale;
+}
+
 // ---------------------------------------------------------------------------------------------
 // main kernel: W waves; wave w owns F feature tiles (16 features each) x TT token tiles. The F
 // tiles come from kBlocks consecutive blocks of the packed layout (F / kBlocks tiles per wave
@@ -156,11 +246,17 @@ __global__ __launch_bounds__(256) void prepare_x_kernel(const bf16_t *x, int ldx
 // workgroup takes several blocks of a one-tile-per-wave layout, so that each activation operand
 // read from LDS feeds several MFMAs.
 // ---------------------------------------------------------------------------------------------
-template <bool kFp8, GemmEpilogue kEpi, int TT, int F, int W, int P, int kBlocks = 1, int kOcc = 1>
+// kScale: Fp8Scaling of the e4m3 operands: 0 tensor (the consumer or the epilogue applies
+// scale(x_amax) * w_scale), 1 channel (the epilogue scales by x_scales[token] * w_scales[feature]),
+// 2 block_128 (each 128-byte K step, one scale block, is accumulated scaled by
+// x_scales(token, step) * w_scales(feature / 128, step)).
+template <bool kFp8, GemmEpilogue kEpi, int TT, int F, int W, int P, int kBlocks = 1, int kOcc = 1,
+          int kScale = 0>
 __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(kOcc)))
 void gemm_kernel(const GemmArgs a) {
   static_assert(F % kBlocks == 0 && (kBlocks == 1 || kEpi != GemmEpilogue::gelu_gate),
                 "blocks per workgroup");
+  static_assert(kScale == 0 || kFp8, "scaled operands are e4m3");
   constexpr int FL = F / kBlocks;  // tiles per wave in the packed layout
   // Activation operand, one LDS stage per K step, filled by DMA (global_load_lds_dwordx4):
   //  - e4m3 weights: the prepared operand (prepare_x_kernel), already in MFMA order, 1 B/element;
@@ -176,7 +272,13 @@ void gemm_kernel(const GemmArgs a) {
   // surplus units repeat the final one (identical bytes to the same LDS address).
   constexpr int kXUnits = kXStage / 1024;
   constexpr int kXDma = (kXUnits + W - 1) / W;  // 16-byte DMA chunks per thread per step
-  constexpr int kLoadsPerStep = kXDma + 2 * F;
+  // block_128: each step also loads the lane's TT activation scales (contiguous), counted in the
+  // in-order vector-memory stream, and the F weight-block scales of its tiles, whose addresses are
+  // wave-uniform (scalar loads, outside that count; were they vector loads, the waits below would
+  // only be stricter).
+  constexpr int kXsVec = TT >= 4 ? 4 : TT;
+  constexpr int kXsLoads = kScale == 2 ? TT / kXsVec : 0;
+  constexpr int kLoadsPerStep = kXDma + 2 * F + kXsLoads;
   __shared__ __attribute__((aligned(16))) unsigned char lds[P * kXStage];
 
   const int lane = threadIdx.x & 63;
@@ -221,6 +323,11 @@ void gemm_kernel(const GemmArgs a) {
     wrow[f] = static_cast<const unsigned char *>(a.w) +
               (static_cast<size_t>(block) * total_steps + step0) * kGroupBytes + tile * kTileBytes + lane * 16;
   }
+  // Weight scale row of tile f (gelu_gate: the up tiles are rows n/2 + feature0).
+  auto scale_row = [&](int f) {
+    if constexpr (kEpi == GemmEpilogue::gelu_gate) return f < F / 2 ? feature0[f] : a.n / 2 + feature0[f];
+    else return feature0[f];
+  };
   // This thread's DMA sources for stage chunk id = unit(i) * 64 + lane. e4m3: the
   // prepared operand, linear. bf16: row id / 8 of X at swizzled position id % 8 (rows past M
   // re-read row M - 1; their outputs are never stored).
@@ -241,6 +348,19 @@ void gemm_kernel(const GemmArgs a) {
   }
 
   u32x4 wreg[P][F][2];
+  float xsreg[P][kScale == 2 ? TT : 1];
+  float wsreg[P][kScale == 2 ? F : 1];
+  const float *xs_src = nullptr;
+  // constant address space: wave-uniform addresses load through the scalar cache (reads only)
+  typedef const __attribute__((address_space(4))) float *const_floats;
+  const_floats ws_src[kScale == 2 ? F : 1];
+  if constexpr (kScale == 2) {
+    xs_src = a.x_scales + ((static_cast<size_t>(m_block) * total_steps + step0) * 16 + col) * TT;
+#pragma unroll
+    for (int f = 0; f < F; ++f)
+      ws_src[f] = reinterpret_cast<const_floats>(reinterpret_cast<uintptr_t>(
+          a.w_scales + static_cast<size_t>(scale_row(f) / 128) * a.w_scale_kblocks + step0));
+  }
   v4f acc[F][TT];
 #pragma unroll
   for (int f = 0; f < F; ++f)
@@ -263,6 +383,23 @@ void gemm_kernel(const GemmArgs a) {
       wreg[slot][f][0] = *reinterpret_cast<const u32x4 *>(src);
       wreg[slot][f][1] = *reinterpret_cast<const u32x4 *>(src + 1024);
     }
+    if constexpr (kScale == 2) {
+      const float *xs = xs_src + static_cast<size_t>(s) * 16 * TT;
+#pragma unroll
+      for (int i = 0; i < kXsLoads; ++i) {
+        if constexpr (kXsVec == 4) {
+          const v4f v = *reinterpret_cast<const v4f *>(xs + i * 4);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) xsreg[slot][i * 4 + e] = v[e];
+        } else {
+          const float2 v = *reinterpret_cast<const float2 *>(xs + i * 2);
+          xsreg[slot][i * 2] = v.x;
+          xsreg[slot][i * 2 + 1] = v.y;
+        }
+      }
+#pragma unroll
+      for (int f = 0; f < F; ++f) wsreg[slot][f] = ws_src[f][s];
+    }
   };
 
   auto mfma = [&](int slot, int f, int j, u32x4 b0, u32x4 b1) {
@@ -275,8 +412,16 @@ void gemm_kernel(const GemmArgs a) {
       const v8i bv = {static_cast<int>(b0.x), static_cast<int>(b0.y), static_cast<int>(b0.z),
                       static_cast<int>(b0.w), static_cast<int>(b1.x), static_cast<int>(b1.y),
                       static_cast<int>(b1.z), static_cast<int>(b1.w)};
-      acc[f][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, acc[f][j], 0, 0, 0, 0,
-                                                                  0, 0);
+      if constexpr (kScale == 2) {
+        const v4f block = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+            av, bv, v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 0, 0, 0);
+        const float sc = xsreg[slot][j] * wsreg[slot][f];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[f][j][e] += block[e] * sc;
+      } else {
+        acc[f][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, acc[f][j], 0, 0, 0, 0,
+                                                                    0, 0);
+      }
     } else {
       acc[f][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
           __builtin_bit_cast(v8bf, a0), __builtin_bit_cast(v8bf, b0), acc[f][j], 0, 0, 0);
@@ -321,7 +466,7 @@ void gemm_kernel(const GemmArgs a) {
   // The output scale's operands are loaded before the weight stream starts and reduced after it,
   // so their latency does not add to the kernel's tail.
   float x_amax_lane = 0.0f, w_scale = 1.0f;
-  if constexpr (kFp8) {
+  if constexpr (kFp8 && kScale == 0) {
     x_amax_lane = amax_lane(a.x_amax, a.amax_stripes);
     w_scale = *a.w_scale;
   }
@@ -345,7 +490,23 @@ void gemm_kernel(const GemmArgs a) {
   }
 
   float out_scale = 1.0f;
-  if constexpr (kFp8) out_scale = fp8_scale_from_amax(wave_max(x_amax_lane)) * w_scale;
+  if constexpr (kFp8 && kScale == 0) out_scale = fp8_scale_from_amax(wave_max(x_amax_lane)) * w_scale;
+  // channel: the lane's token scales and its features' scales
+  float ch_x[kScale == 1 ? TT : 1];
+  v4f ch_w[kScale == 1 ? F : 1];
+  if constexpr (kScale == 1) {
+#pragma unroll
+    for (int j = 0; j < TT; ++j)
+      ch_x[j] = a.x_scales[min(m_block * TT * 16 + col + j * 16, a.m - 1)];
+#pragma unroll
+    for (int f = 0; f < F; ++f) ch_w[f] = *reinterpret_cast<const v4f *>(a.w_scales + scale_row(f) + group * 4);
+  }
+  // output scale of element e of acc[f][j]
+  auto scale_of = [&](int f, int j, int e) -> float {
+    if constexpr (kScale == 1) return ch_x[j] * ch_w[f][e];
+    else if constexpr (kScale == 2) return 1.0f;
+    else return out_scale;
+  };
 
   // ------------------------------------------------------------------ epilogues
   // acc[f][j]: lane (col = token, group g) holds features feature0[f] + 4g + {0..3}.
@@ -357,8 +518,14 @@ void gemm_kernel(const GemmArgs a) {
       if (token >= a.m) continue;
       float *dst = a.partial + (static_cast<size_t>(split) * a.m + token) * a.n;
 #pragma unroll
-      for (int f = 0; f < F; ++f)
-        *reinterpret_cast<v4f *>(dst + feature0[f] + group * 4) = acc[f][j];
+      for (int f = 0; f < F; ++f) {
+        v4f v = acc[f][j];
+        if constexpr (kScale == 1) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] *= scale_of(f, j, e);
+        }
+        *reinterpret_cast<v4f *>(dst + feature0[f] + group * 4) = v;
+      }
     }
   } else if constexpr (kEpi == GemmEpilogue::store_bf16) {
     float amax = 0.0f;
@@ -372,7 +539,7 @@ void gemm_kernel(const GemmArgs a) {
         float v[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          v[e] = acc[f][j][e] * out_scale;
+          v[e] = acc[f][j][e] * scale_of(f, j, e);
           amax = fmaxf(amax, fabsf(v[e]));
         }
         *reinterpret_cast<uint2 *>(dst + feature0[f] + group * 4) =
@@ -398,8 +565,8 @@ void gemm_kernel(const GemmArgs a) {
         float g[4], u[4], v[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          g[e] = acc[f][j][e] * out_scale;
-          u[e] = acc[f + H][j][e] * out_scale;
+          g[e] = acc[f][j][e] * scale_of(f, j, e);
+          u[e] = acc[f + H][j][e] * scale_of(f + H, j, e);
         }
         round_bf16x2(g[0], g[1]);
         round_bf16x2(g[2], g[3]);
@@ -431,7 +598,7 @@ void gemm_kernel(const GemmArgs a) {
       for (int f = 0; f < F; ++f)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const uint64_t key = argmax_key(round_bf16(acc[f][j][e] * out_scale),
+          const uint64_t key = argmax_key(round_bf16(acc[f][j][e] * scale_of(f, j, e)),
                                           static_cast<uint32_t>(feature0[f] + group * 4 + e));
           best = key > best ? key : best;
         }
@@ -481,7 +648,7 @@ __global__ __launch_bounds__(256) void argmax_reduce_kernel(const uint64_t *part
 // Pipeline depth per tiles-per-wave (measured on MI355X: 3 stages suffice from F = 2 on).
 template <int F> constexpr int kStages = F == 1 ? 4 : 3;
 
-template <bool kFp8, GemmEpilogue kEpi, int TT>
+template <bool kFp8, GemmEpilogue kEpi, int TT, int kS>
 void launch_tiles(const GemmArgs &a, bool many, bool group4, dim3 grid, hipStream_t stream) {
   const int w = a.w_layout.waves;
   // Many token blocks (prefill steps): the weights mostly come from L2, and two workgroups per CU
@@ -491,41 +658,50 @@ void launch_tiles(const GemmArgs &a, bool many, bool group4, dim3 grid, hipStrea
     if constexpr (kEpi != GemmEpilogue::gelu_gate) {
       if constexpr (TT == 8) {
         if (group4) {  // four one-tile layout blocks per workgroup
-          if (w == 3) gemm_kernel<kFp8, kEpi, TT, 4, 3, 2, 4, 2><<<grid, 192, 0, stream>>>(a);
-          else gemm_kernel<kFp8, kEpi, TT, 4, 4, 2, 4, 2><<<grid, 256, 0, stream>>>(a);
+          if (w == 3) gemm_kernel<kFp8, kEpi, TT, 4, 3, 2, 4, 2, kS><<<grid, 192, 0, stream>>>(a);
+          else gemm_kernel<kFp8, kEpi, TT, 4, 4, 2, 4, 2, kS><<<grid, 256, 0, stream>>>(a);
           return;
         }
       }
-      if (w == 3) gemm_kernel<kFp8, kEpi, TT, 1, 3, kStages<1>><<<grid, 192, 0, stream>>>(a);
-      else gemm_kernel<kFp8, kEpi, TT, 1, 4, kStages<1>><<<grid, 256, 0, stream>>>(a);
+      if (w == 3) gemm_kernel<kFp8, kEpi, TT, 1, 3, kStages<1>, 1, 1, kS><<<grid, 192, 0, stream>>>(a);
+      else gemm_kernel<kFp8, kEpi, TT, 1, 4, kStages<1>, 1, 1, kS><<<grid, 256, 0, stream>>>(a);
       return;
     }
     break;
   case 2:
-    if (w == 3) gemm_kernel<kFp8, kEpi, TT, 2, 3, kStages<2>><<<grid, 192, 0, stream>>>(a);
-    else gemm_kernel<kFp8, kEpi, TT, 2, 4, kStages<2>><<<grid, 256, 0, stream>>>(a);
+    if (w == 3) gemm_kernel<kFp8, kEpi, TT, 2, 3, kStages<2>, 1, 1, kS><<<grid, 192, 0, stream>>>(a);
+    else gemm_kernel<kFp8, kEpi, TT, 2, 4, kStages<2>, 1, 1, kS><<<grid, 256, 0, stream>>>(a);
     return;
   case 4:
     if constexpr (TT == 8) {
       if (many) {
-        if (w == 3) gemm_kernel<kFp8, kEpi, TT, 4, 3, 2, 1, 2><<<grid, 192, 0, stream>>>(a);
-        else gemm_kernel<kFp8, kEpi, TT, 4, 4, 2, 1, 2><<<grid, 256, 0, stream>>>(a);
+        if (w == 3) gemm_kernel<kFp8, kEpi, TT, 4, 3, 2, 1, 2, kS><<<grid, 192, 0, stream>>>(a);
+        else gemm_kernel<kFp8, kEpi, TT, 4, 4, 2, 1, 2, kS><<<grid, 256, 0, stream>>>(a);
         return;
       }
     }
-    if (w == 3) gemm_kernel<kFp8, kEpi, TT, 4, 3, kStages<4>><<<grid, 192, 0, stream>>>(a);
-    else gemm_kernel<kFp8, kEpi, TT, 4, 4, kStages<4>><<<grid, 256, 0, stream>>>(a);
+    if (w == 3) gemm_kernel<kFp8, kEpi, TT, 4, 3, kStages<4>, 1, 1, kS><<<grid, 192, 0, stream>>>(a);
+    else gemm_kernel<kFp8, kEpi, TT, 4, 4, kStages<4>, 1, 1, kS><<<grid, 256, 0, stream>>>(a);
     return;
   }
   throw std::runtime_error("unsupported weight layout for this GEMM");
 }
 
+template <bool kFp8, GemmEpilogue kEpi, int kS>
+void launch_scaled(const GemmArgs &a, bool small_m, bool group4, dim3 grid, hipStream_t stream) {
+  if (small_m)
+    launch_tiles<kFp8, kEpi, 2, kS>(a, false, group4, grid, stream);
+  else
+    launch_tiles<kFp8, kEpi, 8, kS>(a, a.m > 8 * 16, group4, grid, stream);
+}
+
 template <bool kFp8, GemmEpilogue kEpi>
 void launch_shape(const GemmArgs &a, bool small_m, bool group4, dim3 grid, hipStream_t stream) {
-  if (small_m)
-    launch_tiles<kFp8, kEpi, 2>(a, false, group4, grid, stream);
-  else
-    launch_tiles<kFp8, kEpi, 8>(a, a.m > 8 * 16, group4, grid, stream);
+  if constexpr (kFp8) {
+    if (a.scaling == 1) return launch_scaled<kFp8, kEpi, 1>(a, small_m, group4, grid, stream);
+    if (a.scaling == 2) return launch_scaled<kFp8, kEpi, 2>(a, small_m, group4, grid, stream);
+  }
+  launch_scaled<kFp8, kEpi, 0>(a, small_m, group4, grid, stream);
 }
 
 template <bool kFp8>
@@ -537,8 +713,12 @@ void launch_gemm(const GemmArgs &a, hipStream_t stream) {
   const int row_bytes = a.k * (kFp8 ? 1 : 2);
   if (row_bytes % kStepBytes != 0) throw std::runtime_error("GEMM K must fill 128-byte steps");
   if (a.ldx % 8 != 0) throw std::runtime_error("GEMM activation stride must be 16-byte aligned");
-  if (kFp8 && (a.x_amax == nullptr || a.w_scale == nullptr))
+  if (a.scaling < 0 || a.scaling > 2 || (!kFp8 && a.scaling != 0))
+    throw std::runtime_error("invalid FP8 scaling");
+  if (kFp8 && a.scaling == 0 && (a.x_amax == nullptr || a.w_scale == nullptr))
     throw std::runtime_error("FP8 GEMM needs activation amax and weight scale");
+  if (a.scaling != 0 && (a.w_scales == nullptr || a.x_scales == nullptr || a.xprep_ready))
+    throw std::runtime_error("scaled FP8 GEMM needs weight and activation scale arrays");
   const int total_steps = row_bytes / kStepBytes;
   if (total_steps % a.k_splits != 0) throw std::runtime_error("GEMM split-K must divide K steps");
   const bool small_m = a.m <= 32;
@@ -570,9 +750,22 @@ void launch_gemm(const GemmArgs &a, hipStream_t stream) {
     if (chunks * 16 * m_blocks > a.xprep_capacity)
       throw std::runtime_error("GEMM activation workspace too small");
     const dim3 grid(static_cast<unsigned>((chunks + 255) / 256), m_blocks);
-    if (!a.xprep_ready)
+    if (a.scaling == 1) {
+      if (static_cast<size_t>(m_blocks) * tokens_per_block > a.x_scales_capacity)
+        throw std::runtime_error("GEMM activation scale workspace too small");
+      prepare_x_rows_kernel<<<m_blocks * tokens_per_block, 256, 0, stream>>>(a.x, a.ldx, a.m, a.k, tt,
+                                                                            a.xprep, a.x_scales);
+    } else if (a.scaling == 2) {
+      if (static_cast<size_t>(m_blocks) * total_steps * tokens_per_block > a.x_scales_capacity)
+        throw std::runtime_error("GEMM activation scale workspace too small");
+      if (a.w_scale_kblocks < total_steps) throw std::runtime_error("GEMM weight block scales too few");
+      const dim3 waves_grid(static_cast<unsigned>((total_steps * tt + 3) / 4), m_blocks);
+      prepare_x_blocks_kernel<<<waves_grid, 256, 0, stream>>>(a.x, a.ldx, a.m, a.k, tt, a.xprep,
+                                                             a.x_scales);
+    } else if (!a.xprep_ready) {
       prepare_x_kernel<<<grid, 256, 0, stream>>>(a.x, a.ldx, a.m, a.k, a.x_amax, a.amax_stripes, tt,
                                                a.xprep);
+    }
   }
   // Several token blocks on a one-tile-per-wave layout: a workgroup takes four layout blocks,
   // so that its MFMAs per LDS operand read match the four-tile layouts (measured on MI355X at
@@ -658,6 +851,12 @@ size_t gemm_xprep_bytes(int m, int k) {
   const int tt = gemm_token_tiles(m);
   const int m_blocks = (m + tt * 16 - 1) / (tt * 16);
   return static_cast<size_t>(m_blocks) * (k / kStepBytes) * tt * kTileBytes;
+}
+
+size_t gemm_x_scale_floats(int m, int k) {
+  const int tt = gemm_token_tiles(m);
+  const int m_blocks = (m + tt * 16 - 1) / (tt * 16);
+  return static_cast<size_t>(m_blocks) * tt * 16 * std::max(1, k / kStepBytes);
 }
 
 size_t gemm_argmax_partials(int m, const WeightLayout &layout) {

@@ -73,6 +73,47 @@ __global__ void bf16_amax_kernel(const bf16_t *in, size_t n, float *amax) {
   if ((threadIdx.x & 63) == 0) atomic_max_nonneg(amax, m);
 }
 
+// Fp8Scaling::channel / ::block_128 weights (quantize_bf16_rows_kernel and
+// quantize_weight_block_128_kernel, cuda/linear.cu:300-316, 352-380): one workgroup per row, or
+// per 128 x 128 block; scale = max(amax / 448, 2^-24), q = e4m3(w / scale) (a true division, as
+// the reference's).
+__device__ __forceinline__ float block_max_256(float m) {
+  __shared__ float wave_maxima[4];
+  m = wave_max(m);
+  if ((threadIdx.x & 63) == 0) wave_maxima[threadIdx.x >> 6] = m;
+  __syncthreads();
+  return fmaxf(fmaxf(wave_maxima[0], wave_maxima[1]), fmaxf(wave_maxima[2], wave_maxima[3]));
+}
+
+__global__ __launch_bounds__(256) void quantize_rows_kernel(const bf16_t *in, fp8_t *out, int k,
+                                                            float *scales) {
+  const size_t row = blockIdx.x;
+  const bf16_t *src = in + row * k;
+  float m = 0.0f;
+  for (int c = threadIdx.x; c < k; c += 256) m = fmaxf(m, fabsf(bf16_to_f32(src[c])));
+  const float scale = fmaxf(block_max_256(m) / 448.0f, 0x1p-24f);
+  if (threadIdx.x == 0) scales[row] = scale;
+  for (int c = threadIdx.x; c < k; c += 256)
+    out[row * k + c] = static_cast<fp8_t>(f32x2_to_e4m3x2(bf16_to_f32(src[c]) / scale, 0.0f) & 0xffu);
+}
+
+__global__ __launch_bounds__(256) void quantize_block128_kernel(const bf16_t *in, fp8_t *out, int n,
+                                                                int k, int kbp, float *scales) {
+  const int kb = blockIdx.x, nb = blockIdx.y;
+  const int c = kb * 128 + (threadIdx.x & 127);
+  const int r0 = nb * 128 + (threadIdx.x >> 7);
+  float m = 0.0f;
+  for (int r = r0; r < min(n, nb * 128 + 128); r += 2)
+    if (c < k) m = fmaxf(m, fabsf(bf16_to_f32(in[static_cast<size_t>(r) * k + c])));
+  const float scale = fmaxf(block_max_256(m) / 448.0f, 0x1p-24f);
+  if (threadIdx.x == 0) scales[static_cast<size_t>(nb) * kbp + kb] = scale;
+  for (int r = r0; r < min(n, nb * 128 + 128); r += 2)
+    if (c < k) {
+      const size_t i = static_cast<size_t>(r) * k + c;
+      out[i] = static_cast<fp8_t>(f32x2_to_e4m3x2(bf16_to_f32(in[i]) / scale, 0.0f) & 0xffu);
+    }
+}
+
 __global__ void zero_f32_kernel(float *p) { *p = 0.0f; }
 
 unsigned grid_for(size_t n) {
@@ -103,6 +144,38 @@ void quantize_weight_bf16_to_fp8(const bf16_t *in, fp8_t *out, size_t n, float *
   bf16_amax_kernel<<<grid_for(n), 256, 0, stream>>>(in, n, amax_scratch);
   bf16_to_fp8_weight_kernel<<<grid_for(n), 256, 0, stream>>>(in, out, n, amax_scratch, scale_out);
   hip_check(hipGetLastError(), "launch weight quantisation");
+}
+
+size_t fp8_weight_scale_elements(int scaling, int n, int k) {
+  if (scaling == 0) return 1;
+  if (scaling == 1) return static_cast<size_t>(n);
+  if (scaling == 2) {
+    const size_t kbp = ((static_cast<size_t>(k) + 127) / 128 + 3) & ~static_cast<size_t>(3);
+    return kbp * ((static_cast<size_t>(n) + 127) / 128);
+  }
+  throw std::runtime_error("invalid FP8 scaling");
+}
+
+void quantize_weight_bf16_to_fp8_scaled(const bf16_t *in, fp8_t *out, int n, int k, int scaling,
+                                        float *scales, float *amax_scratch, hipStream_t stream) {
+  if (n <= 0 || k <= 0) throw std::runtime_error("invalid FP8 weight shape");
+  if (scaling == 0) {
+    quantize_weight_bf16_to_fp8(in, out, static_cast<size_t>(n) * k, scales, amax_scratch, stream);
+    return;
+  }
+  if (scaling == 1) {
+    quantize_rows_kernel<<<n, 256, 0, stream>>>(in, out, k, scales);
+  } else if (scaling == 2) {
+    const int kb = (k + 127) / 128;
+    const int kbp = (kb + 3) & ~3;
+    hip_check(hipMemsetAsync(scales, 0, sizeof(float) * fp8_weight_scale_elements(2, n, k), stream),
+              "clear FP8 block weight scales");
+    quantize_block128_kernel<<<dim3(kb, (n + 127) / 128), 256, 0, stream>>>(in, out, n, k, kbp,
+                                                                           scales);
+  } else {
+    throw std::runtime_error("invalid FP8 scaling");
+  }
+  hip_check(hipGetLastError(), "launch scaled weight quantisation");
 }
 
 // cuda/qkv.cu:44-64: sliding tables use theta 1e4 over all D/2 frequencies; the global

@@ -48,6 +48,9 @@ struct ModelSpec {
   AssistantSpec assistant;
   uint64_t seed = 1;
   float weight_std = 0.02f;
+  // Fp8Scaling of the target's e4m3 weights (include/carat/linear.h:27): 0 tensor, 1 channel,
+  // 2 block_128 (Fp8WeightArena::quantize, device_weights.cu:200-263).
+  int fp8_scaling = 0;
 };
 
 // Gemma-4-31B-shaped target at the benchmark's attention shapes: 60 layers, 5 sliding : 1 global,

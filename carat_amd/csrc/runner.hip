@@ -95,6 +95,12 @@ private:
 struct PackedWeight {
   DeviceBuffer data;
   WeightLayout layout;
+  // e4m3 weights under Fp8Scaling channel (1) or block_128 (2): their scales in the
+  // Fp8WeightArena layout ([n], or [ceil(n/128)][scale_kblocks]); tensor-scaled weights keep their
+  // one float with the caller.
+  int scaling = 0;
+  int scale_kblocks = 0;
+  DeviceBuffer scale_table;
   template <typename T> T *as() const { return data.as<T>(); }
   void *get() const { return data.get(); }
 };
@@ -210,7 +216,7 @@ struct BatchModelRunner::Implementation {
 
   // workspaces
   DeviceBuffer hidden_a, hidden_b, normalized, first_residual, pre_mlp, activated, queries,
-      attention_out, final_hidden, partials, amax, argmax_partials, xprep, attention_partials,
+      attention_out, final_hidden, partials, amax, argmax_partials, xprep, x_scales, attention_partials,
       target_hidden, sliding_table, init_scratch;
   size_t attention_partial_floats = 0;
   int attention_chunk_sliding = 256, attention_chunk_global = 256;
@@ -410,7 +416,8 @@ struct BatchModelRunner::Implementation {
 
   // The device source's own e4m3 copy of a segment (Fp8WeightArena) into `dst` and its scale
   // into `scale`; false when the source has none (the bf16 segment is quantised instead).
-  bool copy_device_fp8(const std::string &name, void *dst, size_t bytes, float *scale) {
+  bool copy_device_fp8(const std::string &name, void *dst, size_t bytes, float *scale,
+                       size_t scale_floats = 1) {
     if (device_segment == nullptr) return false;
     const bool assistant = name.rfind("assistant.", 0) == 0;
     const std::string segment = assistant ? name.substr(10) : name;
@@ -424,7 +431,8 @@ struct BatchModelRunner::Implementation {
       throw std::runtime_error("device fp8 weight " + segment + " has no scale");
     hip_check(hipMemcpyAsync(dst, source, bytes, hipMemcpyDeviceToDevice, stream),
               "copy device fp8 weight segment");
-    hip_check(hipMemcpyAsync(scale, source_scale, sizeof(float), hipMemcpyDeviceToDevice, stream),
+    hip_check(hipMemcpyAsync(scale, source_scale, sizeof(float) * scale_floats,
+                             hipMemcpyDeviceToDevice, stream),
               "copy device fp8 weight scale");
     return true;
   }
@@ -449,7 +457,9 @@ struct BatchModelRunner::Implementation {
   void fill_fp8(PackedWeight &w, int n, int k, bool gate_up, uint64_t tensor, float *scale,
                 const std::string &segment) {
     const size_t count = static_cast<size_t>(n) * k;
-    if (copy_device_fp8(segment, staging_for(count), count, scale)) {
+    if (spec.fp8_scaling != 0) {
+      fill_fp8_scaled(w, n, k, tensor, segment);
+    } else if (copy_device_fp8(segment, staging_for(count), count, scale)) {
       // the source's own e4m3 bytes and scale (Fp8WeightArena::quantize already ran)
     } else if (has_source()) {
       if (load_staging.bytes() < count * sizeof(bf16_t)) {
@@ -465,6 +475,30 @@ struct BatchModelRunner::Implementation {
                       spec.weight_std, scale, init_scratch.as<float>(), stream);
     }
     pack_from_staging(w, n, k, gate_up);
+  }
+
+  // The same under Fp8Scaling channel / block_128: the scales go to w.scale_table; the e4m3 bytes
+  // into the staging buffer (the caller packs them).
+  void fill_fp8_scaled(PackedWeight &w, int n, int k, uint64_t tensor, const std::string &segment) {
+    const size_t count = static_cast<size_t>(n) * k;
+    w.scaling = spec.fp8_scaling;
+    const size_t floats = fp8_weight_scale_elements(w.scaling, n, k);
+    w.scale_kblocks = w.scaling == 2 ? static_cast<int>(floats / ((static_cast<size_t>(n) + 127) / 128)) : 0;
+    w.scale_table.allocate(sizeof(float) * floats);
+    if (copy_device_fp8(segment, staging_for(count), count, w.scale_table.as<float>(), floats)) return;
+    if (load_staging.bytes() < count * sizeof(bf16_t)) {
+      hip_check(hipStreamSynchronize(stream), "synchronise before staging growth");
+      load_staging.release();
+      load_staging.allocate(count * sizeof(bf16_t));
+    }
+    if (has_source())
+      upload_segment(segment, load_staging.get(), count * sizeof(bf16_t));
+    else
+      fill_normal_bf16(load_staging.as<bf16_t>(), count, seed_for(tensor), 0.0f, spec.weight_std,
+                       stream);
+    quantize_weight_bf16_to_fp8_scaled(load_staging.as<bf16_t>(), static_cast<fp8_t *>(staging_for(count)),
+                                       n, k, w.scaling, w.scale_table.as<float>(),
+                                       init_scratch.as<float>(), stream);
   }
 
   // bf16 weight [n][k], stored packed. With `fp8`, also its e4m3 copy with a per-tensor scale
@@ -549,6 +583,9 @@ struct BatchModelRunner::Implementation {
       L.capacity = L.spec.sliding ? std::min(maximum_context, spec.sliding_window) : maximum_context;
       L.scales.allocate(4 * sizeof(float));
       float *scales = L.scales.as<float>();
+      // unused under channel / block_128 scaling (the scale tables serve instead)
+      if (spec.fp8_scaling != 0)
+        hip_check(hipMemsetAsync(scales, 0, 4 * sizeof(float), stream), "clear tensor scales");
       const std::string p = "layer." + std::to_string(i) + ".";
       fill_norm(L.input_norm, spec.hidden, tensor++, p + "input_norm");
       fill_norm(L.q_norm, D, tensor++, p + "q_norm");
@@ -583,8 +620,22 @@ struct BatchModelRunner::Implementation {
     fill_bf16(embedding_bf16, static_cast<size_t>(spec.vocabulary) * H, 1, 1.0f, "token_embedding");
     embedding_scale.allocate(sizeof(float));
     const size_t embedding_count = static_cast<size_t>(spec.vocabulary) * H;
-    if (!copy_device_fp8("token_embedding", staging_for(embedding_count), embedding_count,
-                         embedding_scale.as<float>()))
+    if (spec.fp8_scaling != 0) {
+      lm_head.scaling = spec.fp8_scaling;
+      const size_t floats = fp8_weight_scale_elements(lm_head.scaling, spec.vocabulary, spec.hidden);
+      lm_head.scale_kblocks = lm_head.scaling == 2
+                                  ? static_cast<int>(floats / ((static_cast<size_t>(spec.vocabulary) + 127) / 128))
+                                  : 0;
+      lm_head.scale_table.allocate(sizeof(float) * floats);
+      if (!copy_device_fp8("token_embedding", staging_for(embedding_count), embedding_count,
+                           lm_head.scale_table.as<float>(), floats))
+        quantize_weight_bf16_to_fp8_scaled(embedding_bf16.as<bf16_t>(),
+                                           static_cast<fp8_t *>(staging_for(embedding_count)),
+                                           spec.vocabulary, spec.hidden, lm_head.scaling,
+                                           lm_head.scale_table.as<float>(), init_scratch.as<float>(),
+                                           stream);
+    } else if (!copy_device_fp8("token_embedding", staging_for(embedding_count), embedding_count,
+                                embedding_scale.as<float>()))
       quantize_weight_bf16_to_fp8(embedding_bf16.as<bf16_t>(),
                                   static_cast<fp8_t *>(staging_for(embedding_count)),
                                   embedding_count, embedding_scale.as<float>(),
@@ -759,6 +810,12 @@ struct BatchModelRunner::Implementation {
           xp = std::max(xp, gemm_xprep_bytes(batch_size, as.query_heads * L.head_dimension));
       }
       xprep.allocate(xp);
+      if (spec.fp8_scaling != 0) {
+        size_t xs = std::max(gemm_x_scale_floats(step_rows, spec.hidden),
+                             gemm_x_scale_floats(step_rows, spec.intermediate));
+        for (auto &L : layers) xs = std::max(xs, gemm_x_scale_floats(step_rows, L.query_width()));
+        x_scales.allocate(sizeof(float) * xs);
+      }
       size_t keys = gemm_argmax_partials(step_rows, lm_head.layout);
       if (has_assistant) keys = std::max(keys, gemm_argmax_partials(batch_size, a_embedding.layout));
       if (assistant_fp8 != 0) keys = std::max(keys, gemm_argmax_partials(batch_size, a_embedding8.layout));
@@ -873,6 +930,14 @@ struct BatchModelRunner::Implementation {
     g.argmax_out = d_predictions;
     g.xprep = xprep.as<unsigned char>();
     g.xprep_capacity = xprep.bytes();
+    if (w.scaling != 0) {
+      g.scaling = w.scaling;
+      g.w_scales = w.scale_table.as<float>();
+      g.w_scale_kblocks = w.scale_kblocks;
+      g.x_scales = x_scales.as<float>();
+      g.x_scales_capacity = x_scales.bytes() / sizeof(float);
+      g.xprep_ready = false;
+    }
     if (epilogue == GemmEpilogue::partial_f32) g.k_splits = splits_for(w.layout);
     if (splits_out != nullptr) *splits_out = g.k_splits;
     launch_fp8_gemm(g, stream);
@@ -1017,7 +1082,8 @@ struct BatchModelRunner::Implementation {
     // (otherwise the next GEMM prepares its operand itself, with the same bytes).
     auto fuse_quantize = [&](RowArgs &r, int which) {
       r.xprep_token_tiles = gemm_token_tiles(rows);
-      if (!io.fused_quantize || !row_kernel_can_fuse_quantization(r)) return false;
+      if (!io.fused_quantize || spec.fp8_scaling != 0 || !row_kernel_can_fuse_quantization(r))
+        return false;
       r.xprep = xprep.as<unsigned char>();
       r.sync = sync_slot(li, which);
       r.fault = d_fault;
@@ -1027,6 +1093,11 @@ struct BatchModelRunner::Implementation {
     TargetLayer &L = layers[li];
     const float *scales = L.scales.as<float>();
     const int D = L.spec.head_dimension;
+    // Channel / block-scaled GEMMs leave fully scaled partials: their consumers get no scale
+    // operands (scale 1).
+    const bool tensor_scaled = spec.fp8_scaling == 0;
+    auto consumer_amax = [&](const float *x_amax) { return tensor_scaled ? x_amax : nullptr; };
+    auto consumer_scale = [&](int i) { return tensor_scaled ? scales + i : nullptr; };
     // QKV projection
     int splits = 1;
     run_fp8_gemm(io.normalized, rows, spec.hidden, io.in_amax, L.qkv,
@@ -1036,8 +1107,8 @@ struct BatchModelRunner::Implementation {
     q.amax_stripes = kAmaxStripes;
     q.partials = partials.as<float>();
     q.splits = splits;
-    q.x_amax = io.in_amax;
-    q.w_scale = scales + 0;
+    q.x_amax = consumer_amax(io.in_amax);
+    q.w_scale = consumer_scale(0);
     q.rows = rows;
     q.tokens = io.depth;
     q.query_heads = L.spec.query_heads;
@@ -1082,8 +1153,8 @@ struct BatchModelRunner::Implementation {
     ro.eps = spec.eps;
     ro.partials = partials.as<float>();
     ro.splits = splits;
-    ro.x_amax = amax_slot(li, 1);
-    ro.w_scale = scales + 1;
+    ro.x_amax = consumer_amax(amax_slot(li, 1));
+    ro.w_scale = consumer_scale(1);
     ro.w1 = L.post_attention_norm.as<bf16_t>();
     ro.residual = io.input;
     ro.r1_out = first_residual.as<bf16_t>();
@@ -1109,8 +1180,8 @@ struct BatchModelRunner::Implementation {
     rd.eps = spec.eps;
     rd.partials = partials.as<float>();
     rd.splits = splits;
-    rd.x_amax = amax_slot(li, 3);
-    rd.w_scale = scales + 3;
+    rd.x_amax = consumer_amax(amax_slot(li, 3));
+    rd.w_scale = consumer_scale(3);
     rd.w1 = L.post_mlp_norm.as<bf16_t>();
     rd.residual = first_residual.as<bf16_t>();
     rd.scalar = L.scalar.as<bf16_t>();
@@ -1978,6 +2049,8 @@ struct BatchModelRunner::Implementation {
     if (name == "token_embedding") return give(embedding_bf16);
     if (name == "token_embedding.fp8") return give_packed(lm_head);
     if (name == "token_embedding.scale") return give(embedding_scale);
+    // channel / block_128 scales of the e4m3 lm_head and projections (Fp8WeightArena layout)
+    if (name == "token_embedding.scale_table") return give(lm_head.scale_table);
     if (name == "final_norm") return give(final_norm);
     if (name == "target_hidden") return give(target_hidden);
     if (name == "final_hidden") return give(final_hidden);
@@ -2054,6 +2127,10 @@ struct BatchModelRunner::Implementation {
             if (rest == "gate_up") return give_packed(L.gate_up);
             if (rest == "down") return give_packed(L.down);
             if (rest == "scales") return give(L.scales);
+            if (rest == "qkv.scale_table") return give(L.qkv.scale_table);
+            if (rest == "o.scale_table") return give(L.o.scale_table);
+            if (rest == "gate_up.scale_table") return give(L.gate_up.scale_table);
+            if (rest == "down.scale_table") return give(L.down.scale_table);
           } else if (head == "cache") {
             if (rest == "k") return give(L.k_cache);
             if (rest == "v") return give(L.v_cache);

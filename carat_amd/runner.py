@@ -42,6 +42,9 @@ class ModelDesc:
     # AssistantFp8Mode (assistant_runner.cu:29-43): None reads CARAT_ASSISTANT_FP8_MODE as the
     # reference does (unset: off); else "off", "lm_head" or "all"
     assistant_fp8_mode: str | None = None
+    # Fp8Scaling of the target's e4m3 weights (include/carat/linear.h:27): "tensor", "channel"
+    # or "block_128"
+    fp8_scaling: str = "tensor"
 
     @staticmethod
     def gemma4_benchmark(with_assistant: bool = True) -> "ModelDesc":
@@ -75,6 +78,10 @@ class ModelDesc:
         if self.assistant_fp8_mode not in modes:
             raise ValueError("assistant_fp8_mode must be None, 'off', 'lm_head' or 'all'")
         d.assistant_fp8_mode = modes[self.assistant_fp8_mode]
+        scalings = {"tensor": 0, "channel": 1, "block_128": 2}
+        if self.fp8_scaling not in scalings:
+            raise ValueError("fp8_scaling must be 'tensor', 'channel' or 'block_128'")
+        d.fp8_scaling = scalings[self.fp8_scaling]
         return d, arr
 
 

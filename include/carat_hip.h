@@ -81,6 +81,13 @@ typedef struct carat_hip_model_desc {
    * assistant FP8 arena (segment(..., assistant = 1, fp8 = 1, ...)) and otherwise fails with
    * "assistant FP8 mode requires quantized assistant weights". */
   int assistant_fp8_mode;
+  /* Fp8Scaling of the target's e4m3 weights (include/carat/linear.h:27, Fp8WeightArena::quantize
+   * device_weights.cu:200-263): 0 tensor, 1 channel, 2 block_128. Under channel / block_128 each
+   * projection and the lm_head quantise their activations per row / per 1 x 128 block
+   * (run_decode_linear, layer_runner.cu:220-238) and scale inside the GEMM; a runner over device
+   * weights copies the arena's scale arrays (n floats, or ceil(n/128) x kbp, kbp = ceil(k/128)
+   * rounded up to 4). */
+  int fp8_scaling;
 } carat_hip_model_desc;
 
 typedef struct carat_hip_runner carat_hip_runner;
@@ -286,6 +293,22 @@ int carat_hip_argmax_accept_noalloc(const float *logits_f32, const uint16_t *log
 int carat_hip_fp8_linear(const uint16_t *x, int m, int k, const float *x_amax, const uint8_t *w,
                          int n, const float *w_scale, int epilogue, int splits, uint16_t *y,
                          float *y_amax, float *partial, int32_t *predictions, void *stream);
+/* run_decode_linear under Fp8Scaling::channel (1) / ::block_128 (2) (layer_runner.cu:220-238):
+ * x bf16 [m][k] quantised per row (quantize_bf16_rows, linear.cu:300-316) or per 1 x 128 block
+ * (quantize_activation_block_128_kernel, linear.cu:382-401), then Fp8Linear::run with OUTER_VEC /
+ * VEC128 x BLK128x128 scales (linear.cu:706-717): w e4m3 [n][k], w_scales [n] or
+ * [ceil(n/128)][kbp] (carat_hip_quantize_weight_fp8). Epilogues as carat_hip_fp8_linear; the
+ * partials (epilogue 1) carry the full scale. */
+int carat_hip_fp8_linear_scaled(const uint16_t *x, int m, int k, int fp8_scaling, const uint8_t *w,
+                                int n, const float *w_scales, int epilogue, int splits, uint16_t *y,
+                                float *partial, int32_t *predictions, void *stream);
+/* fp8_weight_block_scale_elements (linear.cu:403-409) and its tensor / channel counterparts: the
+ * scale floats of an [n][k] weight under fp8_scaling 0 / 1 / 2 (1, n, ceil(n/128) x kbp). */
+int carat_hip_fp8_weight_scale_elements(int fp8_scaling, int n, int k, uint64_t *out);
+/* Fp8WeightArena::quantize of one bf16 [n][k] segment (device_weights.cu:240-256): e4m3 [n][k]
+ * row-major and its scales, per tensor (amax/448), row or 128 x 128 block (max(amax/448, 2^-24)). */
+int carat_hip_quantize_weight_fp8(const uint16_t *w, int n, int k, int fp8_scaling, uint8_t *out,
+                                  float *scales, void *stream);
 /* No reference counterpart (cuBLASLt picks its own algorithm, linear.cu:53-72): the storage layout
  * (tiles per wave, waves per workgroup) and split-K factor the runner uses for an [n][k] weight,
  * so op-level calls can reproduce the runner's exact dispatch. */

@@ -322,6 +322,112 @@ void orc_fp8_lm_head_argmax(const uint16_t *x, int m, int k, const uint8_t *qw, 
 }
 
 /* ------------------------------------------------------------------------------------------ */
+/* Fp8Scaling::channel and ::block_128 (include/carat/linear.h:27, cuda/linear.cu:300-420,      */
+/* 706-717; Fp8WeightArena::quantize device_weights.cu:222-256; run_decode_linear                */
+/* layer_runner.cu:220-238). Every scale is max(amax / 448, 2^-24) and q = e4m3(x / scale):     */
+/*  - channel: one scale per weight row [n] and per activation row [m] (quantize_bf16_rows);   */
+/*  - block_128: one scale per 128 x 128 weight block, [ceil(n/128)][kbp] with kbp =           */
+/*    ceil(k/128) rounded up to a multiple of 4 (padding zeroed), and one per 1 x 128           */
+/*    activation block, [ceil(k/128)][m];                                                      */
+/* Y[m][n] = bf16(sum over K blocks b of (sx(m, b) * sw(n, b)) * sum_{k in b} qx * qw), with   */
+/* channel as the one-block case (sx(m), sw(n)).                                               */
+/* ------------------------------------------------------------------------------------------ */
+
+static float scaled_block_scale(float amax) { return fmaxf(amax / 448.0f, 0x1p-24f); }
+
+/* quantize_bf16_rows_kernel (linear.cu:300-316): rows x width, scales[rows] */
+void orc_quantize_e4m3_rows(const uint16_t *x, int rows, int width, uint8_t *q, float *scales) {
+#pragma omp parallel for schedule(static)
+  for (int r = 0; r < rows; ++r) {
+    const uint16_t *xr = x + (int64_t)r * width;
+    float amax = 0.0f;
+    for (int c = 0; c < width; ++c) amax = fmaxf(amax, fabsf(orc_bf16_to_f32(xr[c])));
+    const float scale = scaled_block_scale(amax);
+    scales[r] = scale;
+    for (int c = 0; c < width; ++c) q[(int64_t)r * width + c] = orc_f32_to_e4m3(orc_bf16_to_f32(xr[c]) / scale);
+  }
+}
+
+int64_t orc_fp8_weight_block_scale_elements(int n, int k) {
+  const int64_t kb = (k + 127) / 128;
+  return ((kb + 3) & ~(int64_t)3) * ((n + 127) / 128);
+}
+
+/* quantize_weight_block_128_kernel (linear.cu:352-380): w [n][k] */
+void orc_quantize_e4m3_weight_block128(const uint16_t *w, int n, int k, uint8_t *q, float *scales) {
+  const int kb_count = (k + 127) / 128, kbp = (kb_count + 3) & ~3, nb_count = (n + 127) / 128;
+  memset(scales, 0, sizeof(float) * (size_t)kbp * nb_count);
+#pragma omp parallel for collapse(2) schedule(static)
+  for (int nb = 0; nb < nb_count; ++nb)
+    for (int kb = 0; kb < kb_count; ++kb) {
+      float amax = 0.0f;
+      for (int r = nb * 128; r < n && r < nb * 128 + 128; ++r)
+        for (int c = kb * 128; c < k && c < kb * 128 + 128; ++c)
+          amax = fmaxf(amax, fabsf(orc_bf16_to_f32(w[(int64_t)r * k + c])));
+      const float scale = scaled_block_scale(amax);
+      scales[(int64_t)nb * kbp + kb] = scale;
+      for (int r = nb * 128; r < n && r < nb * 128 + 128; ++r)
+        for (int c = kb * 128; c < k && c < kb * 128 + 128; ++c)
+          q[(int64_t)r * k + c] = orc_f32_to_e4m3(orc_bf16_to_f32(w[(int64_t)r * k + c]) / scale);
+    }
+}
+
+/* quantize_activation_block_128_kernel (linear.cu:382-401): x [rows][k], scales[kb][rows] */
+void orc_quantize_e4m3_activation_block128(const uint16_t *x, int rows, int k, uint8_t *q,
+                                           float *scales) {
+  const int kb_count = (k + 127) / 128;
+#pragma omp parallel for schedule(static)
+  for (int r = 0; r < rows; ++r)
+    for (int kb = 0; kb < kb_count; ++kb) {
+      const uint16_t *xr = x + (int64_t)r * k;
+      float amax = 0.0f;
+      for (int c = kb * 128; c < k && c < kb * 128 + 128; ++c) amax = fmaxf(amax, fabsf(orc_bf16_to_f32(xr[c])));
+      const float scale = scaled_block_scale(amax);
+      scales[(int64_t)kb * rows + r] = scale;
+      for (int c = kb * 128; c < k && c < kb * 128 + 128; ++c)
+        q[(int64_t)r * k + c] = orc_f32_to_e4m3(orc_bf16_to_f32(xr[c]) / scale);
+    }
+}
+
+/* Fp8Linear::run with OUTER_VEC (channel) or VEC128 x BLK128x128 (block_128) scales
+ * (linear.cu:706-717): fp32 out[m][n]; each block's dot product is exact in double, scaled by
+ * the fp32 product sx * sw and summed in double. scaling: 1 channel, 2 block_128. */
+void orc_fp8_linear_scaled_f32(const uint8_t *qx, const float *sx, const uint8_t *qw,
+                               const float *sw, int m, int k, int n, int scaling, float *out) {
+  float table[256];
+  for (int i = 0; i < 256; ++i) table[i] = orc_e4m3_to_f32((uint8_t)i);
+  const int kb_count = (k + 127) / 128, kbp = (kb_count + 3) & ~3;
+#pragma omp parallel for schedule(static)
+  for (int col = 0; col < n; ++col) {
+    const uint8_t *wr = qw + (int64_t)col * k;
+    for (int row = 0; row < m; ++row) {
+      const uint8_t *xr = qx + (int64_t)row * k;
+      double total = 0.0;
+      if (scaling == 1) {
+        double acc = 0.0;
+        for (int c = 0; c < k; ++c) acc += (double)table[xr[c]] * table[wr[c]];
+        total = (double)((float)acc * (sx[row] * sw[col]));
+      } else {
+        for (int kb = 0; kb < kb_count; ++kb) {
+          double acc = 0.0;
+          for (int c = kb * 128; c < k && c < kb * 128 + 128; ++c) acc += (double)table[xr[c]] * table[wr[c]];
+          total += acc * (double)(sx[(int64_t)kb * m + row] * sw[(int64_t)(col / 128) * kbp + kb]);
+        }
+      }
+      out[(int64_t)row * n + col] = (float)total;
+    }
+  }
+}
+
+void orc_fp8_linear_scaled(const uint8_t *qx, const float *sx, const uint8_t *qw, const float *sw,
+                           int m, int k, int n, int scaling, uint16_t *out) {
+  float *tmp = (float *)malloc(sizeof(float) * (size_t)m * n);
+  orc_fp8_linear_scaled_f32(qx, sx, qw, sw, m, k, n, scaling, tmp);
+  for (int64_t i = 0; i < (int64_t)m * n; ++i) out[i] = orc_f32_to_bf16(tmp[i]);
+  free(tmp);
+}
+
+/* ------------------------------------------------------------------------------------------ */
 /* row ops: cuda/ops.cu:27-217 (RMSNorm variants), 228-284 (GELU gate), 321-335 (embedding)     */
 /* ------------------------------------------------------------------------------------------ */
 

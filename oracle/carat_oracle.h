@@ -78,6 +78,19 @@ void orc_fp8_linear_f32(const uint8_t *qx, float sx, const uint8_t *qw, float sw
 /* Bf16Linear::run (linear.cu:534-643): bf16 output of an fp32-accumulated GEMM. */
 void orc_bf16_linear(const uint16_t *x, const uint16_t *w, int m, int k, int n, uint16_t *out);
 /* lm_head restatement: quantize x, fp8 GEMM, bf16 logits, argmax. */
+/* Fp8Scaling::channel / ::block_128 (linear.cu:300-420, 706-717): scale = max(amax/448, 2^-24),
+ * q = e4m3(x / scale). Row scales [rows]; weight block scales [ceil(n/128)][kbp] (kbp = ceil(k/128)
+ * rounded up to 4, padding 0); activation block scales [ceil(k/128)][rows]. scaling 1 channel,
+ * 2 block_128. */
+void orc_quantize_e4m3_rows(const uint16_t *x, int rows, int width, uint8_t *q, float *scales);
+int64_t orc_fp8_weight_block_scale_elements(int n, int k);
+void orc_quantize_e4m3_weight_block128(const uint16_t *w, int n, int k, uint8_t *q, float *scales);
+void orc_quantize_e4m3_activation_block128(const uint16_t *x, int rows, int k, uint8_t *q,
+                                           float *scales);
+void orc_fp8_linear_scaled_f32(const uint8_t *qx, const float *sx, const uint8_t *qw,
+                               const float *sw, int m, int k, int n, int scaling, float *out);
+void orc_fp8_linear_scaled(const uint8_t *qx, const float *sx, const uint8_t *qw, const float *sw,
+                           int m, int k, int n, int scaling, uint16_t *out);
 void orc_fp8_lm_head_argmax(const uint16_t *x, int m, int k, const uint8_t *qw, float sw, int n,
                             int32_t *argmax_out, uint16_t *logits_out /* nullable */);
 

@@ -202,6 +202,71 @@ def bf16_linear(x_bf16, w_bf16) -> np.ndarray:
     return out
 
 
+SCALING = {"tensor": 0, "channel": 1, "block_128": 2}
+
+
+def quantize_e4m3_rows(x_bf16):
+    """quantize_bf16_rows (Fp8Scaling::channel): q, scales[rows]."""
+    x = c(x_bf16, np.uint16)
+    rows, width = x.shape
+    q = np.empty(x.shape, np.uint8)
+    s = np.empty(rows, np.float32)
+    lib().orc_quantize_e4m3_rows(p(x), rows, width, p(q), p(s))
+    return q, s
+
+
+def quantize_e4m3_weight_block128(w_bf16):
+    """quantize_bf16_weight_to_fp8_block_128: q, scales[ceil(n/128) * kbp] (flat)."""
+    w = c(w_bf16, np.uint16)
+    n, k = w.shape
+    q = np.empty(w.shape, np.uint8)
+    lib().orc_fp8_weight_block_scale_elements.restype = c_int64
+    s = np.empty(lib().orc_fp8_weight_block_scale_elements(n, k), np.float32)
+    lib().orc_quantize_e4m3_weight_block128(p(w), n, k, p(q), p(s))
+    return q, s
+
+
+def quantize_e4m3_activation_block128(x_bf16):
+    """quantize_bf16_activation_to_fp8_block_128: q, scales[ceil(k/128)][rows] (flat)."""
+    x = c(x_bf16, np.uint16)
+    rows, k = x.shape
+    q = np.empty(x.shape, np.uint8)
+    s = np.empty(((k + 127) // 128) * rows, np.float32)
+    lib().orc_quantize_e4m3_activation_block128(p(x), rows, k, p(q), p(s))
+    return q, s
+
+
+def quantize_weight_scaled(w_bf16, scaling):
+    """Fp8WeightArena::quantize of one segment under `scaling` (0/1/2): q, scales (flat)."""
+    if scaling == 0:
+        q, s = quantize_e4m3(w_bf16)
+        return q, np.array([s], np.float32)
+    return quantize_e4m3_rows(w_bf16) if scaling == 1 else quantize_e4m3_weight_block128(w_bf16)
+
+
+def quantize_activation_scaled(x_bf16, scaling):
+    """run_decode_linear's activation quantisation under `scaling` (0/1/2): q, scales (flat)."""
+    if scaling == 0:
+        q, s = quantize_e4m3(x_bf16)
+        return q, np.array([s], np.float32)
+    return quantize_e4m3_rows(x_bf16) if scaling == 1 else quantize_e4m3_activation_block128(x_bf16)
+
+
+def fp8_linear_scaled(qx, sx, qw, sw, scaling, f32=False) -> np.ndarray:
+    """Fp8Linear::run under `scaling` (0 tensor, 1 channel, 2 block_128)."""
+    qx = c(qx, np.uint8)
+    qw = c(qw, np.uint8)
+    if scaling == 0:
+        f = fp8_linear_f32 if f32 else fp8_linear
+        return f(qx, float(np.ravel(sx)[0]), qw, float(np.ravel(sw)[0]))
+    m, k = qx.shape
+    n = qw.shape[0]
+    out = np.empty((m, n), np.float32 if f32 else np.uint16)
+    fn = lib().orc_fp8_linear_scaled_f32 if f32 else lib().orc_fp8_linear_scaled
+    fn(p(qx), p(c(sx, np.float32)), p(qw), p(c(sw, np.float32)), m, k, n, scaling, p(out))
+    return out
+
+
 def fp8_lm_head_argmax(x_bf16, qw, sw):
     x = c(x_bf16, np.uint16)
     qw = c(qw, np.uint8)

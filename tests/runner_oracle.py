@@ -12,14 +12,28 @@ import numpy as np
 from oracle import oracle
 
 
-def layer_weights(runner, i):
+SCALINGS = {"tensor": 0, "channel": 1, "block_128": 2}
+
+
+def layer_weights(runner, i, scaling=0):
     names = ["input_norm", "q_norm", "k_norm", "post_attention_norm", "pre_mlp_norm",
              "post_mlp_norm", "scalar"]
     w = {n: runner.read(f"layer.{i}.{n}", np.uint16) for n in names}
-    for n in ("qkv", "o", "gate_up", "down"):
+    tensor_scales = runner.read(f"layer.{i}.scales", np.float32)
+    for j, n in enumerate(("qkv", "o", "gate_up", "down")):
         w[n] = runner.read(f"layer.{i}.{n}", np.uint8)
-    w["scales"] = runner.read(f"layer.{i}.scales", np.float32)
+        # the weight's scales: one float (tensor), or its channel / block_128 table
+        w[n + ".scales"] = (tensor_scales[j:j + 1] if scaling == 0 else
+                            runner.read(f"layer.{i}.{n}.scale_table", np.float32))
+    w["scales"] = tensor_scales
     return w
+
+
+def projection(x, qw, sw, scaling):
+    """run_decode_linear (layer_runner.cu:220-238) under the arena's Fp8Scaling: the activation
+    quantised per tensor / row / 1 x 128 block, then Fp8Linear::run."""
+    qx, sx = oracle.quantize_activation_scaled(x, scaling)
+    return oracle.fp8_linear_scaled(qx, sx, qw, sw, scaling)
 
 
 def verify_step(runner, desc, batch, capacity_of, proposals, slots, positions, head_rows=None):
@@ -34,19 +48,20 @@ def verify_step(runner, desc, batch, capacity_of, proposals, slots, positions, h
     rows = R * T
     emb = runner.read("token_embedding", np.uint16).reshape(desc.vocabulary, H)
     emb_q = runner.read("token_embedding.fp8", np.uint8).reshape(desc.vocabulary, H)
-    emb_s = float(runner.read("token_embedding.scale", np.float32)[0])
+    scaling = SCALINGS[getattr(desc, "fp8_scaling", "tensor")]
+    emb_s = (runner.read("token_embedding.scale", np.float32)[:1] if scaling == 0 else
+             runner.read("token_embedding.scale_table", np.float32))
     final_norm = runner.read("final_norm", np.uint16)
     rowpos = (np.asarray(positions, np.int32)[:, None] + np.arange(T, dtype=np.int32)[None, :]).reshape(-1)
     hidden = oracle.embedding(emb, proposals.reshape(-1), math.sqrt(H))
-    weights = [layer_weights(runner, i) for i in range(len(desc.layers))]
+    weights = [layer_weights(runner, i, scaling) for i in range(len(desc.layers))]
     x, _ = oracle.rms_norm(hidden, weights[0]["input_norm"], eps=desc.rms_norm_epsilon)
     out = {"k_new": [], "v_new": [], "attention": []}
     for li, spec in enumerate(desc.layers):
         w = weights[li]
         D, hq, hkv = spec.head_dimension, spec.query_heads, spec.kv_heads
         C = capacity_of(li)
-        qx, sx = oracle.quantize_e4m3(x)
-        packed = oracle.fp8_linear(qx, sx, w["qkv"].reshape(-1, H), float(w["scales"][0]))
+        packed = projection(x, w["qkv"].reshape(-1, H), w["qkv.scales"], scaling)
         cos = runner.read("rope.sliding.cos" if spec.sliding else "rope.global.cos", np.uint16).reshape(-1, D)
         sin = runner.read("rope.sliding.sin" if spec.sliding else "rope.global.sin", np.uint16).reshape(-1, D)
         q, k, v = oracle.qkv_post(packed, w["q_norm"], w["k_norm"], cos, sin, rowpos, hq, hkv, D,
@@ -59,22 +74,23 @@ def verify_step(runner, desc, batch, capacity_of, proposals, slots, positions, h
         attn = oracle.verify_attention(q.reshape(R, T, hq, D), kc, vc, k.reshape(R, T, hkv, D),
                                        v.reshape(R, T, hkv, D), slots, positions, C, window)
         out["attention"].append(attn)
-        qa, sa = oracle.quantize_e4m3(attn.reshape(rows, hq * D))
-        proj = oracle.fp8_linear(qa, sa, w["o"].reshape(H, hq * D), float(w["scales"][1]))
+        proj = projection(attn.reshape(rows, hq * D), w["o"].reshape(H, hq * D), w["o.scales"], scaling)
         r1, pre, _ = oracle.rms_norm_add_and_norm(proj, w["post_attention_norm"], hidden,
                                                   w["pre_mlp_norm"], desc.rms_norm_epsilon)
-        qp, sp = oracle.quantize_e4m3(pre)
-        gu = oracle.fp8_linear(qp, sp, w["gate_up"].reshape(2 * desc.intermediate, H), float(w["scales"][2]))
+        gu = projection(pre, w["gate_up"].reshape(2 * desc.intermediate, H), w["gate_up.scales"], scaling)
         act, _ = oracle.gelu_tanh_gate_rows(gu)
-        qd, sd = oracle.quantize_e4m3(act)
-        down = oracle.fp8_linear(qd, sd, w["down"].reshape(H, desc.intermediate), float(w["scales"][3]))
+        down = projection(act, w["down"].reshape(H, desc.intermediate), w["down.scales"], scaling)
         hidden = oracle.rms_norm_add_scale(down, w["post_mlp_norm"], r1, int(w["scalar"][0]),
                                            desc.rms_norm_epsilon)
         nxt = weights[li + 1]["input_norm"] if li + 1 < len(desc.layers) else final_norm
         x, _ = oracle.rms_norm(hidden, nxt, eps=desc.rms_norm_epsilon)
     out["final_hidden"] = x
-    pred, logits = oracle.fp8_lm_head_argmax(x if head_rows is None else x[np.asarray(head_rows)],
-                                             emb_q, emb_s)
+    head_x = x if head_rows is None else x[np.asarray(head_rows)]
+    if scaling == 0:
+        pred, logits = oracle.fp8_lm_head_argmax(head_x, emb_q, float(emb_s[0]))
+    else:  # batch_model_runner.cu:840-853: the final hidden quantised per row / block
+        logits = projection(head_x, emb_q, emb_s, scaling)
+        pred = oracle.argmax_bf16_rows(logits)
     out["predictions"] = pred
     out["logits"] = logits
     return out

@@ -272,3 +272,64 @@ def test_assistant_fp8_arena_from_device_weights(loaded, torch_cuda, monkeypatch
         assert [row[0] for row in drafts] == [5, 6, 7, 8]
     finally:
         other.close()
+
+
+@pytest.mark.parametrize("scaling", ["channel", "block_128"])
+def test_scaled_fp8_weights_from_device_segments(loaded, torch_cuda, scaling):
+    """Fp8WeightArena::quantize with Fp8Scaling::channel / ::block_128 (device_weights.cu:222-256):
+    from bf16 device segments the runner quantises each projection and the lm_head itself, bit for
+    bit the oracle's quantisation of the checkpoint bytes; given an arena, it takes the arena's
+    e4m3 bytes and scale arrays (here the oracle's at twice the input, so the scales differ from
+    the runner's own), and a verify step over them runs."""
+    import dataclasses
+
+    torch = torch_cuda
+    runner, cfg, tensors, a_tensors = loaded
+    desc = dataclasses.replace(runner._desc, fp8_scaling=scaling)
+    mode = {"channel": 1, "block_128": 2}[scaling]
+    host = plan_segments(cfg, tensors, a_tensors)
+    dev = {k: torch.from_numpy(np.ascontiguousarray(v).view(np.int16)).cuda() for k, v in host.items()}
+    addresses = {k: v.data_ptr() for k, v in dev.items()}
+    names = ["token_embedding"] + [f"layer.{li}.{n}" for li in range(len(desc.layers))
+                                   for n in ("qkv", "o", "gate_up", "down")]
+
+    def fp8_name(name):
+        return name + (".fp8" if name == "token_embedding" else "")
+
+    say(f"case: {scaling} runner quantising bf16 device segments")
+    other = BatchModelRunner.from_device_weights(desc, addresses, BATCH, MAX_CONTEXT)
+    try:
+        for name in names:
+            q, s = oracle.quantize_weight_scaled(host[(False, name)], mode)
+            assert np.array_equal(other.read(fp8_name(name), np.uint8), q.reshape(-1)), name
+            assert np.array_equal(other.read(name + ".scale_table", np.float32), s), name
+    finally:
+        other.close()
+    say(f"case: {scaling} runner over an arena's e4m3 segments and scale arrays")
+    fp8, keep = {}, []
+    for name in names:
+        m = host[(False, name)]
+        q, s = oracle.quantize_weight_scaled(oracle.f32_to_bf16(oracle.bf16_to_f32(m) * 2.0), mode)
+        dq = torch.from_numpy(np.ascontiguousarray(q)).cuda()
+        ds = torch.from_numpy(s).cuda()
+        keep += [dq, ds]
+        fp8[(False, name)] = (dq.data_ptr(), ds.data_ptr(), q, s)
+    other = BatchModelRunner.from_device_weights(desc, addresses, BATCH, MAX_CONTEXT,
+                                                 {k: v[:2] for k, v in fp8.items()})
+    try:
+        for name in names:
+            q, s = fp8[(False, name)][2:]
+            assert np.array_equal(other.read(fp8_name(name), np.uint8), q.reshape(-1)), name
+            assert np.array_equal(other.read(name + ".scale_table", np.float32), s), name
+        other.seed_random_cache(60, seed=24, stddev=1 / math.sqrt(128))
+        props = np.random.default_rng(10).integers(0, desc.vocabulary, (4, 5))
+        positions = np.full(4, 60, np.int32)
+        expect = verify_step(other, desc, BATCH, lambda li: min(MAX_CONTEXT, desc.sliding_window)
+                             if desc.layers[li].sliding else MAX_CONTEXT, props, [0, 1, 2, 3], positions)
+        other.verify_greedy_proposals(props.tolist(), props[:, 0].tolist(), [0, 1, 2, 3], [0] * 4)
+        pred = np.array(other.last_predictions, np.int32)
+        logits = oracle.bf16_to_f32(expect["logits"]).astype(np.float64).reshape(len(pred), -1)
+        gap = logits.max(1) - logits[np.arange(len(pred)), pred]
+        assert np.all(gap <= 2 * 2 ** -7 * np.abs(logits).max(1))
+    finally:
+        other.close()

@@ -215,6 +215,99 @@ def test_fp8_linear_against_float64_matmul():
     assert np.allclose(got, expect, rtol=1e-6, atol=1e-6 * np.abs(expect).max())
 
 
+# ------------------------------------------------------------------ channel / block_128 scaling
+def _planted_blocks(rows, cols, block_rows, block_cols, rng):
+    """bf16 matrix whose (block_rows x block_cols) blocks each hold one planted maximum of a
+    distinct magnitude, so that every block's amax (and scale) is known in closed form."""
+    x = rng.uniform(-1, 1, (rows, cols)).astype(np.float32)
+    nb, kb = -(-rows // block_rows), -(-cols // block_cols)
+    amax = np.zeros((nb, kb))
+    for i in range(nb):
+        for j in range(kb):
+            big = 2.0 + i * 3.5 + j * 1.25  # bf16-exact values > 1
+            r = i * block_rows + (i + j) % min(block_rows, rows - i * block_rows)
+            c = j * block_cols + (2 * i + j) % min(block_cols, cols - j * block_cols)
+            x[r, c] = -big if (i + j) % 2 else big
+            amax[i, j] = big
+    return oracle.f32_to_bf16(x), amax
+
+
+def _dequantised(q, scale_of_element):
+    return oracle.e4m3_table().astype(np.float64)[q] * scale_of_element
+
+
+def test_row_quantisation_closed_form():
+    rng = np.random.default_rng(21)
+    x, amax = _planted_blocks(9, 300, 1, 300, rng)
+    x[4] = 0  # an all-zero row takes the 2^-24 floor and quantises to zeros
+    q, s = oracle.quantize_e4m3_rows(x)
+    expect = np.float32(amax[:, 0]).astype(np.float32) / np.float32(448.0)
+    expect[4] = np.float32(2.0 ** -24)
+    assert np.array_equal(s, expect)
+    assert not q[4].any()
+    xf = oracle.bf16_to_f32(x).astype(np.float64)
+    # q = e4m3(x / scale) with a true float32 division; the planted maximum lands on +-448
+    direct = np.array([[oracle.f32_to_e4m3_scalar(float(np.float32(v) / s[r])) for v in xf[r]]
+                       for r in range(9)], np.uint8)
+    assert np.array_equal(q, direct)
+    assert np.all(np.isin(q[np.abs(xf) == amax[:, :1]], [0x7E, 0xFE]))
+    rel = np.abs(_dequantised(q, s[:, None].astype(np.float64)) - xf)
+    assert np.all(rel <= np.abs(xf) * 2 ** -4 + s[:, None] * 2 ** -9 * 0.5 + 1e-30)
+
+
+def test_weight_block128_quantisation_layout():
+    rng = np.random.default_rng(22)
+    for n, k in ((200, 300), (128, 512), (37, 129)):
+        w, amax = _planted_blocks(n, k, 128, 128, rng)
+        q, s = oracle.quantize_e4m3_weight_block128(w)
+        nb, kb = amax.shape
+        kbp = (kb + 3) // 4 * 4
+        assert s.shape == (nb * kbp,)
+        grid = s.reshape(nb, kbp)
+        assert np.array_equal(grid[:, :kb], (amax.astype(np.float32) / np.float32(448.0)))
+        assert not grid[:, kb:].any()  # padding columns stay zero
+        per_element = np.repeat(np.repeat(grid[:, :kb].astype(np.float64), 128, 0), 128, 1)[:n, :k]
+        xf = oracle.bf16_to_f32(w).astype(np.float64)
+        assert np.all(np.abs(_dequantised(q, per_element) - xf) <= np.abs(xf) * 2 ** -4 + per_element * 2 ** -10)
+
+
+def test_activation_block128_quantisation_layout():
+    rng = np.random.default_rng(23)
+    x, amax = _planted_blocks(5, 384, 1, 128, rng)
+    q, s = oracle.quantize_e4m3_activation_block128(x)
+    # [k block][row]
+    assert np.array_equal(s.reshape(3, 5), (amax.T.astype(np.float32) / np.float32(448.0)))
+    per_element = np.repeat(s.reshape(3, 5).T.astype(np.float64), 128, 1)
+    xf = oracle.bf16_to_f32(x).astype(np.float64)
+    assert np.all(np.abs(_dequantised(q, per_element) - xf) <= np.abs(xf) * 2 ** -4 + per_element * 2 ** -10)
+
+
+@pytest.mark.parametrize("scaling", [1, 2])
+def test_scaled_fp8_linear_against_dequantised_float64_matmul(scaling):
+    """Scales factor out of each block's dot product, so the block-scaled sum equals the float64
+    product of the dequantised operands; a transposed or shifted scale index fails this."""
+    rng = np.random.default_rng(24 + scaling)
+    m, k, n = 6, 384, 260
+    x = oracle.f32_to_bf16(rng.standard_normal((m, k)) * np.exp(rng.uniform(-2, 2, (m, 1))))
+    w = oracle.f32_to_bf16(rng.standard_normal((n, k)) * 0.05 * np.exp(rng.uniform(-2, 2, (n, 1))))
+    qw, sw = oracle.quantize_weight_scaled(w, scaling)
+    qx, sx = oracle.quantize_activation_scaled(x, scaling)
+    if scaling == 1:
+        xs, ws = sx[:, None].astype(np.float64), sw[:, None].astype(np.float64)
+    else:
+        kb = k // 128
+        xs = np.repeat(sx.reshape(kb, m).T.astype(np.float64), 128, 1)
+        ws = np.repeat(np.repeat(sw.reshape(-1, (kb + 3) // 4 * 4)[:, :kb].astype(np.float64), 128, 0), 128, 1)[:n]
+    expect = _dequantised(qx, xs) @ _dequantised(qw, ws).T
+    got = oracle.fp8_linear_scaled(qx, sx, qw, sw, scaling, f32=True).astype(np.float64)
+    assert np.allclose(got, expect, rtol=1e-6, atol=1e-6 * np.abs(expect).max())
+    # and the quantised product stays close to the bf16 one (the scales are not misapplied)
+    exact = oracle.bf16_to_f32(x).astype(np.float64) @ oracle.bf16_to_f32(w).astype(np.float64).T
+    assert np.abs(got - exact).max() <= 0.08 * np.abs(exact).max()
+    bf = oracle.bf16_to_f32(oracle.fp8_linear_scaled(qx, sx, qw, sw, scaling)).astype(np.float64)
+    assert np.all(np.abs(bf - got) <= np.abs(got) * 2 ** -8 * 1.01 + 1e-30)
+
+
 # ------------------------------------------------------------------ row ops
 def _bf(x):
     return oracle.bf16_to_f32(oracle.f32_to_bf16(x)).astype(np.float64)
