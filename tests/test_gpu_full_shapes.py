@@ -574,3 +574,28 @@ def test_config5_deep_prefill_step_full_dimensions(full_model):
             assert err <= 3e-2 and rms <= 1e-2, (li, kind)
     assert runner.slot_position(slot) == p + rows
 
+
+
+@pytest.mark.parametrize("scaling", ["channel", "block_128"])
+def test_config5_scaled_fp8_verify_step_full_dimensions(torch_cuda, scaling):
+    """The verify step over channel / block_128-scaled weights (Fp8Scaling, linear.h:27) at
+    config-5 dimensions: every projection and the lm_head quantise their activations per row /
+    per 1 x 128 block and scale inside the GEMM (run_decode_linear, layer_runner.cu:220-238);
+    same bars as the per-tensor step."""
+    desc = ModelDesc(hidden=H, intermediate=INTER, vocabulary=VOCAB, sliding_window=1024,
+                     layers=[LayerSpec(True), LayerSpec(False)], seed=8, weight_std=0.02,
+                     fp8_scaling=scaling)
+    say(f"case: full-dimension {scaling} runner create")
+    runner = BatchModelRunner(desc, SLOTS, MAX_CONTEXT)
+    try:
+        rng = np.random.default_rng(59)
+        positions_by_slot = rng.integers(1024, MAX_CONTEXT - T + 1, SLOTS).astype(np.int32)
+        runner.seed_random_cache(int(positions_by_slot.max()), seed=9, stddev=1 / math.sqrt(128))
+        for slot, p in enumerate(positions_by_slot):
+            runner.set_slot_position(slot, int(p))
+        slots = rng.permutation(SLOTS).astype(np.int32)
+        first = rng.integers(0, VOCAB, SLOTS).astype(np.int32)
+        full_verify_case(runner, desc, slots, positions_by_slot[slots], first, T, None, rng,
+                         f"config-5 {scaling}")
+    finally:
+        runner.close()
