@@ -556,6 +556,8 @@ def main() -> int:
     ap.add_argument("--assistant-fp8", choices=["off", "lm_head", "all"], default=None,
                     help="the assistant's AssistantFp8Mode (default: CARAT_ASSISTANT_FP8_MODE, "
                          "as the reference reads it; unset = off)")
+    ap.add_argument("--fp8-scaling", choices=["tensor", "channel", "block_128"], default="tensor",
+                    help="Fp8Scaling of the target's e4m3 weights (the reference serves per tensor)")
     ap.add_argument("--no-breakdown", action="store_true",
                     help="skip the per-kernel-family probe of one verify step (kernels_ms_per_verify)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -609,6 +611,7 @@ def main() -> int:
     desc = (ModelDesc.gemma4_31b(with_assistant=True) if args.native
             else ModelDesc.gemma4_benchmark(with_assistant=True))
     desc.assistant_fp8_mode = args.assistant_fp8
+    desc.fp8_scaling = args.fp8_scaling
     assistant_fp8 = args.assistant_fp8 or os.environ.get("CARAT_ASSISTANT_FP8_MODE") or "off"
     total = args.warmup + args.steps
     # config 5's 8192-token contexts; the cache holds the rows the warmup, timed and probe steps
@@ -712,6 +715,7 @@ def main() -> int:
             "contexts": ("seeded KV values" if args.seeded_cache
                          else "prefilled from seeded random token ids"),
             "graphs": bool(args.graphs), "assistant_fp8_mode": assistant_fp8,
+            "fp8_scaling": args.fp8_scaling,
             "mean_accepted_per_step": round(accepted_total / steps, 2),
             "draft_ms": round(draft_ms / steps, 3), "verify_ms": round(verify_ms / steps, 3),
         },

@@ -412,16 +412,8 @@ void gemm_kernel(const GemmArgs a) {
       const v8i bv = {static_cast<int>(b0.x), static_cast<int>(b0.y), static_cast<int>(b0.z),
                       static_cast<int>(b0.w), static_cast<int>(b1.x), static_cast<int>(b1.y),
                       static_cast<int>(b1.z), static_cast<int>(b1.w)};
-      if constexpr (kScale == 2) {
-        const v4f block = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-            av, bv, v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 0, 0, 0);
-        const float sc = xsreg[slot][j] * wsreg[slot][f];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) acc[f][j][e] += block[e] * sc;
-      } else {
-        acc[f][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, acc[f][j], 0, 0, 0, 0,
-                                                                    0, 0);
-      }
+      acc[f][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, acc[f][j], 0, 0, 0, 0,
+                                                                  0, 0);
     } else {
       acc[f][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
           __builtin_bit_cast(v8bf, a0), __builtin_bit_cast(v8bf, b0), acc[f][j], 0, 0, 0);
@@ -444,9 +436,26 @@ void gemm_kernel(const GemmArgs a) {
     }
   };
 
+  // block_128: one step's product of weight tile f and token tile j, unscaled (a fresh
+  // accumulator); its scale xs(token, step) * ws(f, step) is applied one token tile later, so that
+  // the multiply-adds of tile j - 1 run under tile j's MFMAs.
+  auto mfma_block = [&](int slot, int f, u32x4 b0, u32x4 b1) -> v4f {
+    const u32x4 a0 = wreg[slot][f][0];
+    const u32x4 a1 = wreg[slot][f][1];
+    const v8i av = {static_cast<int>(a0.x), static_cast<int>(a0.y), static_cast<int>(a0.z),
+                    static_cast<int>(a0.w), static_cast<int>(a1.x), static_cast<int>(a1.y),
+                    static_cast<int>(a1.z), static_cast<int>(a1.w)};
+    const v8i bv = {static_cast<int>(b0.x), static_cast<int>(b0.y), static_cast<int>(b0.z),
+                    static_cast<int>(b0.w), static_cast<int>(b1.x), static_cast<int>(b1.y),
+                    static_cast<int>(b1.z), static_cast<int>(b1.w)};
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, v4f{0.f, 0.f, 0.f, 0.f}, 0, 0,
+                                                           0, 0, 0, 0);
+  };
+
   auto compute = [&](int slot) {
     u32x4 c0 = b_operand(slot, 0, 0);
     u32x4 c1 = b_operand(slot, 0, 1);
+    v4f pending[kScale == 2 ? F : 1];
 #pragma unroll
     for (int j = 0; j < TT; ++j) {
       u32x4 n0 = c0, n1 = c1;
@@ -455,11 +464,35 @@ void gemm_kernel(const GemmArgs a) {
         n1 = b_operand(slot, j + 1, 1);
       }
       __builtin_amdgcn_sched_barrier(0);
+      if constexpr (kScale == 2) {
+        v4f current[F];
 #pragma unroll
-      for (int f = 0; f < F; ++f) mfma(slot, f, j, c0, c1);
+        for (int f = 0; f < F; ++f) current[f] = mfma_block(slot, f, c0, c1);
+        if (j > 0) {
+#pragma unroll
+          for (int f = 0; f < F; ++f) {
+            const float sc = xsreg[slot][j - 1] * wsreg[slot][f];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[f][j - 1][e] += pending[f][e] * sc;
+          }
+        }
+#pragma unroll
+        for (int f = 0; f < F; ++f) pending[f] = current[f];
+      } else {
+#pragma unroll
+        for (int f = 0; f < F; ++f) mfma(slot, f, j, c0, c1);
+      }
       __builtin_amdgcn_sched_barrier(0);
       c0 = n0;
       c1 = n1;
+    }
+    if constexpr (kScale == 2) {
+#pragma unroll
+      for (int f = 0; f < F; ++f) {
+        const float sc = xsreg[slot][TT - 1] * wsreg[slot][f];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[f][TT - 1][e] += pending[f][e] * sc;
+      }
     }
   };
 
@@ -656,7 +689,8 @@ void launch_tiles(const GemmArgs &a, bool many, bool group4, dim3 grid, hipStrea
   switch (a.w_layout.tiles_per_wave) {
   case 1:
     if constexpr (kEpi != GemmEpilogue::gelu_gate) {
-      if constexpr (TT == 8) {
+      // (block_128 keeps one workgroup per CU: its per-step scale registers would spill at two)
+      if constexpr (TT == 8 && kS != 2) {
         if (group4) {  // four one-tile layout blocks per workgroup
           if (w == 3) gemm_kernel<kFp8, kEpi, TT, 4, 3, 2, 4, 2, kS><<<grid, 192, 0, stream>>>(a);
           else gemm_kernel<kFp8, kEpi, TT, 4, 4, 2, 4, 2, kS><<<grid, 256, 0, stream>>>(a);
@@ -673,7 +707,7 @@ void launch_tiles(const GemmArgs &a, bool many, bool group4, dim3 grid, hipStrea
     else gemm_kernel<kFp8, kEpi, TT, 2, 4, kStages<2>, 1, 1, kS><<<grid, 256, 0, stream>>>(a);
     return;
   case 4:
-    if constexpr (TT == 8) {
+    if constexpr (TT == 8 && kS != 2) {
       if (many) {
         if (w == 3) gemm_kernel<kFp8, kEpi, TT, 4, 3, 2, 1, 2, kS><<<grid, 192, 0, stream>>>(a);
         else gemm_kernel<kFp8, kEpi, TT, 4, 4, 2, 1, 2, kS><<<grid, 256, 0, stream>>>(a);
@@ -770,7 +804,7 @@ void launch_gemm(const GemmArgs &a, hipStream_t stream) {
   // Several token blocks on a one-tile-per-wave layout: a workgroup takes four layout blocks,
   // so that its MFMAs per LDS operand read match the four-tile layouts (measured on MI355X at
   // 1024 rows: the one-tile workgroup is bound by its LDS operand reads).
-  const bool group4 = m_blocks > 1 && a.w_layout.tiles_per_wave == 1 && blocks_n % 4 == 0 &&
+  const bool group4 = m_blocks > 1 && a.scaling != 2 && a.w_layout.tiles_per_wave == 1 && blocks_n % 4 == 0 &&
                       (a.epilogue == GemmEpilogue::partial_f32 || a.epilogue == GemmEpilogue::store_bf16);
   const int wg_blocks = group4 ? blocks_n / 4 : blocks_n;
   const int64_t groups = (static_cast<int64_t>(wg_blocks) * a.k_splits + 7) / 8;
