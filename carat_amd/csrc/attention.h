@@ -53,7 +53,9 @@ struct AttentionArgs {
   // arguments over the projection's split-K partials) done by the attention kernel itself, each
   // workgroup for its (request, kv head): the query rows go straight into the workgroup, this
   // step's K/V rows (and a global layer's cache rows) are written before any key is read, and
-  // `q` is not read. Only where attention_can_fuse_qkv holds.
+  // `q` is not read. Decode steps (the assistant): the query-only post-processing, the rows also
+  // written to `q` (= qkv.q_out) by the pair's first key chunk. Only where attention_can_fuse_qkv
+  // holds.
   bool fuse_qkv = false;
   QkvArgs qkv;
 };
@@ -65,8 +67,10 @@ int attention_default_chunk(AttentionMode mode, int max_keys, int requests, int 
 void launch_attention(const AttentionArgs &args, hipStream_t stream);
 // Whether launch_attention can run `args` with fuse_qkv: a verify step (sliding or global) at
 // D = 128 with bf16 K/V, <= 16 query rows per kv head and <= 8 tokens, one key chunk per
-// (request, kv head), and `qkv` the matching QKV post-processing over 1-4 split-K partials of an
-// fp8 projection, with no position offset.
+// (request, kv head), and `qkv` the matching QKV post-processing over 1-2 split-K partials of an
+// fp8 projection, with no position offset; or a one-row decode step at D = 128 with bf16 K/V
+// whose `qkv` is the query-only post-processing (kv_heads 0) of 1-2 partials, bf16 (no scale
+// operands) or fp8, writing its rows to `q`.
 bool attention_can_fuse_qkv(const AttentionArgs &args);
 
 }  // namespace carat_hip

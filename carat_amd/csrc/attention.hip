@@ -88,7 +88,11 @@ constexpr int kAttentionOccupancy = D <= 128 ? (NQ == 1 ? 3 : 2) : D <= 256 ? 2 
 constexpr int kFusedQkvMaxTokens = 8;
 constexpr int kFusedQkvUnitsPerWave = 8;
 
-template <int D, int S>
+// kQueryOnly: the assistant's decode step, whose projection holds only query heads (it reads the
+// target's cache): units are the query rows, the RoPE position is p + position_offset + t, bf16
+// projections carry no scale operands (scale 1), and the rows also go to q_out (written by the
+// first key chunk of the pair) for the stage checks.
+template <int D, int S, bool kQueryOnly = false>
 struct FusedQkv {
   static constexpr int E = D / 64;
   static constexpr int U = kFusedQkvUnitsPerWave;
@@ -109,16 +113,19 @@ struct FusedQkv {
     kind = u < G * T ? 0 : 1 + (u - G * T) / T;
     t = u < G * T ? u % T : (u - G * T) % T;
   }
+  __device__ __forceinline__ static int unit_count(const QkvArgs &q, int G, int T) {
+    return kQueryOnly ? G * T : G * T + (q.key_equals_value ? 1 : 2) * T;
+  }
 
   __device__ __forceinline__ void load(const AttentionArgs &a, int r, int h, int p) {
     const QkvArgs &q = a.qkv;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
     const int hq = a.query_heads, hkv = a.kv_heads, G = hq / hkv, T = a.tokens;
     const int query_width = hq * D, kv_width = hkv * D;
-    const int packed_width = query_width + kv_width * (q.key_equals_value ? 1 : 2);
-    const int units = G * T + (q.key_equals_value ? 1 : 2) * T;
-    amax_part = amax_lane(q.x_amax, q.amax_stripes);
-    w_scale = *q.w_scale;
+    const int packed_width = kQueryOnly ? query_width : query_width + kv_width * (q.key_equals_value ? 1 : 2);
+    const int units = unit_count(q, G, T);
+    amax_part = q.x_amax != nullptr ? amax_lane(q.x_amax, q.amax_stripes) : 0.0f;
+    w_scale = q.w_scale != nullptr ? *q.w_scale : 1.0f;
     // Branch-free: past the last unit a wave re-loads the last one (its values are not used), so
     // no control-flow merge makes the compiler wait for these loads before the K/V stages go out.
 #pragma unroll
@@ -138,7 +145,7 @@ struct FusedQkv {
         part[i][k][0] = v.x;
         part[i][k][1] = v.y;
       }
-      const size_t rope = static_cast<size_t>(p + t) * D + lane * E;
+      const size_t rope = static_cast<size_t>(p + q.position_offset + t) * D + lane * E;
       unpack(load_u32((kind == 1 ? q.k_norm : q.q_norm) + lane * E), wv[i]);
       unpack(load_u32(q.cosine + rope), cs[i]);
       unpack(load_u32(q.sine + rope), sn[i]);
@@ -146,12 +153,13 @@ struct FusedQkv {
   }
 
   __device__ __forceinline__ void finish(const AttentionArgs &a, int r, int h, int p, int slot,
-                                         bf16_t *q_tile) {
+                                         bf16_t *q_tile, bool store_q = false) {
     const QkvArgs &q = a.qkv;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
     const int hq = a.query_heads, hkv = a.kv_heads, G = hq / hkv, T = a.tokens;
-    const int units = G * T + (q.key_equals_value ? 1 : 2) * T;
-    const float scale = w_scale * fp8_scale_from_amax(wave_max(amax_part));
+    const int units = unit_count(q, G, T);
+    const float scale =
+        q.x_amax != nullptr ? w_scale * fp8_scale_from_amax(wave_max(amax_part)) : w_scale;
     // per unit: split-K sum, bf16, RMSNorm (Q, K with weight; V without), RoPE (Q, K). The
     // arithmetic of every unit comes first, branch-free (both the rotated and the plain result),
     // so the units' dependency chains interleave; past the last unit a wave redoes the last one.
@@ -198,9 +206,15 @@ struct FusedQkv {
               cache + ((static_cast<size_t>(slot) * hkv + h) * q.capacity + (p + t) % q.capacity) * D +
               lane * E) = vals;
       };
-      if (kind == 0)
+      if (kind == 0) {
         *reinterpret_cast<uint32_t *>(q_tile + u * D + lane * E) = roped[i];
-      else if (kind == 1)
+        if (kQueryOnly && store_q)
+          *reinterpret_cast<uint32_t *>(
+              q.q_out + (static_cast<size_t>(row) * hq + h * G + u / T) * D + lane * E) = roped[i];
+        continue;
+      }
+      if (kQueryOnly) continue;
+      if (kind == 1)
         write_kv(q.k_new, q.k_cache, roped[i]);
       if (kind == 2 || (kind == 1 && q.key_equals_value)) write_kv(q.v_new, q.v_cache, plain[i]);
     }
@@ -378,14 +392,16 @@ void attention_kernel(const AttentionArgs a) {
   // With the QKV post-processing fused, this step's K/V rows are written by the workgroup itself
   // first, and only stages issued after those stores may read them (key >= p).
   constexpr bool kFuseQkv = kFuseSplits > 0;
-  FusedQkv<(kFuseSplits > 0 ? D : 128), (kFuseSplits > 0 ? kFuseSplits : 1)> fused;
+  // decode: the assistant's query-only projection (no K/V rows to store)
+  constexpr bool kQueryOnly = kMode == AttentionMode::decode;
+  FusedQkv<(kFuseSplits > 0 ? D : 128), (kFuseSplits > 0 ? kFuseSplits : 1), kQueryOnly> fused;
   // Fused QKV: every wave's loads of stages 0 .. 2 kStages - 3 (the early ones and those issued
   // in loop iterations 0 .. kStages - 2) stay below p when the range starts 2 kStages - 2
   // strides before it; the K/V rows' stores then need no wait of their own: a wave's in-order
   // memory counter has retired them once iteration kStages - 2 waited for its stage, and the
   // workgroup barrier at iteration kStages - 1 makes that so for every wave before any fresh key
   // is loaded. For shorter ranges the early stages are issued again after the stores.
-  const bool kv_async = kFuseQkv && chunk_lo + (2 * kStages - 2) * stride <= p;
+  const bool kv_async = kFuseQkv && (kQueryOnly || chunk_lo + (2 * kStages - 2) * stride <= p);
   if constexpr (kFuseQkv) {
     // The prologue's loads go out before the stages (so that waiting for them does not wait for
     // the stages), and the stages unconditionally: a branch here would merge into a full wait.
@@ -404,10 +420,10 @@ void attention_kernel(const AttentionArgs a) {
   u32x4 *q_lds = reinterpret_cast<u32x4 *>(lds + kWaves * kWaveBytes);
   int row_t[NQ];
   if constexpr (kFuseQkv) {
-    static_assert(NQ == 1 && !kQInLds && !kFp8 && kMode != AttentionMode::decode, "fused QKV shape");
+    static_assert(NQ == 1 && !kQInLds && !kFp8, "fused QKV shape");
     // the query rows [qr = local_head * T + t][D] bf16, in LDS of their own
     bf16_t *q_tile = reinterpret_cast<bf16_t *>(lds + kLdsBytes - kQTileBytes);
-    fused.finish(a, r, h, p, slot, q_tile);
+    fused.finish(a, r, h, p, slot, q_tile, chunk == 0);
     if (kv_async) {
       wait_lgkmcnt0();  // the query rows are in LDS (the K/V stores stay in flight)
       __builtin_amdgcn_s_barrier();
@@ -615,7 +631,7 @@ void attention_kernel(const AttentionArgs a) {
         const int it = it0 + j;
         if (it >= iterations) break;
         // fused QKV: every wave's K/V row stores have retired (see kv_async)
-        if (kFuseQkv && kv_async && it == kStages - 1) __builtin_amdgcn_s_barrier();
+        if (kFuseQkv && !kQueryOnly && kv_async && it == kStages - 1) __builtin_amdgcn_s_barrier();
         __asm__ volatile("" ::: "memory");  // the previous iteration's LDS reads stay above
         if constexpr (kStages > 1) issue(it + kStages - 1, (j + kStages - 1) % kStages);
         wait_vmcnt<(kStages - 1) * kLoadsPerStage>();
@@ -1144,6 +1160,9 @@ void launch_fused(const AttentionArgs &a, dim3 grid, hipStream_t stream) {
   if (a.mode == AttentionMode::sliding)
     attention_kernel<128, 1, false, AttentionMode::sliding, kAttentionWaves, S>
         <<<grid, kAttentionWaves * 64, 0, stream>>>(a);
+  else if (a.mode == AttentionMode::decode)
+    attention_kernel<128, 1, false, AttentionMode::decode, kAttentionWaves, S>
+        <<<grid, kAttentionWaves * 64, 0, stream>>>(a);
   else
     attention_kernel<128, 1, false, AttentionMode::global, kAttentionWaves, S>
         <<<grid, kAttentionWaves * 64, 0, stream>>>(a);
@@ -1158,14 +1177,14 @@ void launch_typed(const AttentionArgs &a, dim3 grid, hipStream_t stream) {
         launch_fused<1>(a, grid, stream);
       else
         launch_fused<2>(a, grid, stream);
-      if (a.timing_stop != nullptr) hip_check(hipEventRecord(a.timing_stop, stream), "record probe");
-      return;
     }
   }
-  if (a.fp8_kv)
-    launch_mode<D, NQ, true>(a, grid, stream);
-  else
-    launch_mode<D, NQ, false>(a, grid, stream);
+  if (!a.fuse_qkv) {
+    if (a.fp8_kv)
+      launch_mode<D, NQ, true>(a, grid, stream);
+    else
+      launch_mode<D, NQ, false>(a, grid, stream);
+  }
   if (a.timing_stop != nullptr) hip_check(hipEventRecord(a.timing_stop, stream), "record probe");
   if ((a.max_keys + a.chunk_keys - 1) / a.chunk_keys > 1) {
     const int qrows = (a.query_heads / a.kv_heads) * a.tokens;
@@ -1182,6 +1201,17 @@ void launch_typed(const AttentionArgs &a, dim3 grid, hipStream_t stream) {
 
 bool attention_can_fuse_qkv(const AttentionArgs &a) {
   const QkvArgs &q = a.qkv;
+  if (a.mode == AttentionMode::decode) {
+    // the assistant's query-only projection, one row per request, any number of key chunks
+    const int G = a.kv_heads > 0 ? a.query_heads / a.kv_heads : 0;
+    return a.dimension == 128 && !a.fp8_kv && G > 0 && G <= 16 && a.tokens == 1 &&
+           G <= kAttentionWaves * kFusedQkvUnitsPerWave && a.chunk_keys > 0 &&
+           q.partials != nullptr && (q.splits == 1 || q.splits == 2) &&
+           (q.x_amax == nullptr) == (q.w_scale == nullptr) && q.kv_heads == 0 &&
+           q.rows == a.requests && q.tokens == 1 && q.query_heads == a.query_heads &&
+           q.dimension == 128 && q.q_norm != nullptr && q.cosine != nullptr && q.sine != nullptr &&
+           q.positions == a.positions && q.q_out != nullptr && q.q_out == a.q;
+  }
   const int G = a.kv_heads > 0 ? a.query_heads / a.kv_heads : 0;
   const int units = G * a.tokens + (q.key_equals_value ? 1 : 2) * a.tokens;
   return (a.mode == AttentionMode::sliding || a.mode == AttentionMode::global) && a.dimension == 128 &&

@@ -1791,7 +1791,6 @@ struct BatchModelRunner::Implementation {
     q.positions = a_context;
     q.position_offset = step;
     q.q_out = a_queries.as<bf16_t>();
-    launch_qkv_post(q, stream);
     AttentionArgs at;
     at.mode = AttentionMode::decode;
     at.q = a_queries.as<bf16_t>();
@@ -1812,6 +1811,10 @@ struct BatchModelRunner::Implementation {
     at.amax_stripes = stripes;
     at.partials = attention_partials.as<float>();
     at.chunk_keys = L.attention_chunk;
+    // the query post-processing inside the decode attention where it can run there
+    at.qkv = q;
+    at.fuse_qkv = qkv_fusion && attention_can_fuse_qkv(at);
+    if (!at.fuse_qkv) launch_qkv_post(q, stream);
     launch_attention(at, stream);
     splits = run_assistant_partial(a_attention_out.as<bf16_t>(), active, qw, L.o, L.o8,
                                    all8 ? scales8 + 1 : nullptr, assistant_layer_amax(step, li, 1));

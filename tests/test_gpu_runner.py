@@ -235,6 +235,35 @@ def test_qkv_fusion_equals_the_separate_kernel(model):
         assert np.array_equal(a, b), name
 
 
+@pytest.mark.parametrize("mode", ["off", "all"])
+def test_draft_query_fusion_equals_the_separate_kernel(torch_cuda, mode):
+    """The assistant's decode attention post-processes its own query rows (norm, RoPE at
+    p + step; bf16 projections unscaled, `all` mode with the per-tensor scale) with the QKV
+    kernel's arithmetic: proposals and every intermediate the draft leaves equal the separate
+    kernel's bit for bit, the global layer's two key chunks included."""
+    desc = tiny_desc()
+    desc.assistant_fp8_mode = mode
+    say(f"case: fused vs separate assistant query post-processing, fp8 mode {mode}")
+    runner = BatchModelRunner(desc, BATCH, MAX_CONTEXT)
+    try:
+        names = ["assistant.queries", "assistant.attention_out", "assistant.previous_hidden",
+                 "assistant.final_hidden"]
+        out = []
+        for fused in (True, False):
+            reset_state(runner, [30, 60, 90, 120], seed=19)
+            runner.set_qkv_fusion(fused)
+            try:
+                drafts = runner.draft_four([5, 6, 7, 8], [3, 1, 0, 2], [], 4)
+                out.append((drafts, [runner.read(n, np.uint16).copy() for n in names]))
+            finally:
+                runner.set_qkv_fusion(True)
+        assert out[0][0] == out[1][0]
+        for name, a, b in zip(names, out[0][1], out[1][1]):
+            assert np.array_equal(a, b), name
+    finally:
+        runner.close()
+
+
 def test_fused_quantization_wait_timeout_is_an_error(model):
     """A layer-end workgroup whose wait for the agreed amax runs out sets a fault flag; the step
     raises instead of returning results from a partly quantised operand. Forced from the host with
