@@ -34,12 +34,13 @@ constexpr float kLog2e = 1.4426950408889634f;
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) { return f32x2_to_bf16x2(lo, hi); }
 
-// e4m3 -> bf16 is exact (bf16 has the wider exponent and mantissa): the hardware converts a
-// pair of e4m3 bytes to two floats, and the bf16 pair is their high halves (one byte permute).
+// e4m3 -> bf16 is exact (bf16 has the wider exponent and mantissa): gfx950 converts a pair of
+// e4m3 bytes straight to a bf16 pair (unit scale; checked on MI355X against the float route for
+// every code).
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
 template <bool kHigh>
 __device__ __forceinline__ uint32_t e4m3x2_to_bf16x2(uint32_t word) {
-  const auto f = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(word), kHigh);
-  return __builtin_amdgcn_perm(__float_as_uint(f[1]), __float_as_uint(f[0]), 0x07060302u);
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(word, 1.0f, kHigh));
 }
 
 // 8 e4m3 bytes -> 8 bf16 (exact).
@@ -480,28 +481,24 @@ void attention_kernel(const AttentionArgs a) {
   }
 
   const float score_scale = kFp8 ? a.k_scale * kLog2e : kLog2e;  // scores kept in log2 units
-  // Per-lane LDS offsets inside a V stage, fixed for the whole loop: V[key 4*group + e][d =
-  // dt*16 + col] of tile kt. The swizzle XORs the chunk index with key % kChunksPerRow < 16, which
-  // touches only the chunk's low log2(kXorSpan) bits, so the offsets repeat every kVPeriod output
-  // tiles shifted by kXorSpan chunks: one period is kept in registers, the rest are immediates.
+  // V^T operand. Row i of output tile dt stands for d = i * DT + dt (the output rows are
+  // permuted the same way), so lane (i = col, group g) needs, of each key row 4g + e, the DT
+  // contiguous elements from d = col * DT on: per block of 8 tiles, one wide LDS read per key row
+  // (16 bytes of bf16, 8 of e4m3) instead of one read per element. Per-lane offsets inside a V
+  // stage, fixed for the whole loop (swizzled chunk positions, see the DMA).
   static_assert(KT == 1, "one 16-key tile per wave iteration");
-  constexpr int kXorSpan = kChunksPerRow < 16 ? kChunksPerRow : 16;
-  constexpr int kVPeriodRaw = kXorSpan / (kFp8 ? 1 : 2);
-  constexpr int kVPeriod = kVPeriodRaw < DT ? kVPeriodRaw : DT;
-  static_assert(DT % kVPeriod == 0, "V offset period");
-  int v_base[KT][4][kVPeriod];
+  static_assert(DT % 8 == 0, "V operand blocks of 8 tiles");
+  constexpr int kVBlocks = DT / 8;
+  constexpr int kEltBytes = kFp8 ? 1 : 2;
+  int v_off[4][kVBlocks];
 #pragma unroll
-  for (int kt = 0; kt < KT; ++kt) {
+  for (int e = 0; e < 4; ++e)
 #pragma unroll
-    for (int e = 0; e < 4; ++e)
-#pragma unroll
-      for (int dt = 0; dt < kVPeriod; ++dt) {
-        const int key = kt * 16 + 4 * group + e;
-        const int byte = (dt * 16 + col) * (kFp8 ? 1 : 2);
-        v_base[kt][e][dt] =
-            key * kSrcRowBytes + (((byte >> 4) ^ (key % kChunksPerRow)) << 4) + (byte & 15);
-      }
-  }
+    for (int b = 0; b < kVBlocks; ++b) {
+      const int key = 4 * group + e;
+      const int byte = (col * DT + 8 * b) * kEltBytes;
+      v_off[e][b] = key * kSrcRowBytes + (((byte >> 4) ^ (key % kChunksPerRow)) << 4) + (byte & 15);
+    }
 
   // K operand of MFMA step s from the K slices of stage st (bf16; e4m3 widened exactly).
   auto k_operand = [&](int st, int s) -> u32x4 {
@@ -510,13 +507,25 @@ void attention_kernel(const AttentionArgs a) {
     else
       return kreg[st][s];
   };
-  // bf16 bits of V[key 4*group + e of tile kt][d = dt*16 + col].
-  auto v_element = [&](const unsigned char *vst, int kt, int e, int dt) -> uint32_t {
-    const int at = v_base[kt][e][dt % kVPeriod] + (dt / kVPeriod) * kXorSpan * 16;
-    if constexpr (kFp8)
-      return __float_as_uint(e4m3_to_f32(vst[at])) >> 16;
-    else
-      return *reinterpret_cast<const uint16_t *>(vst + at);
+  // A operands of tiles 8b .. 8b + 7: pairs[j] = {V[4g][d], V[4g+1][d]}, {V[4g+2][d], V[4g+3][d]}
+  // (bf16) at d = col * DT + 8b + j; e4m3 rows are widened exactly first.
+  auto v_block = [&](const unsigned char *vst, int b, u32x2 (&pairs)[8]) {
+    u32x4 raw[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if constexpr (kFp8)
+        raw[e] = e4m3x8_to_bf16x8(*reinterpret_cast<const u32x2 *>(vst + v_off[e][b]));
+      else
+        raw[e] = *reinterpret_cast<const u32x4 *>(vst + v_off[e][b]);
+    }
+    {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
+        pairs[j] = u32x2{__builtin_amdgcn_perm(raw[1][j / 2], raw[0][j / 2], sel),
+                         __builtin_amdgcn_perm(raw[3][j / 2], raw[2][j / 2], sel)};
+      }
+    }
   };
   auto process = [&](int kbase, int st, const unsigned char *vst) {
     // ---- scores S^T[key][qrow] (log2 units)
@@ -599,7 +608,7 @@ void attention_kernel(const AttentionArgs a) {
     // ---- O^T[d][qrow] += V^T[d][keys] . P^T[keys][qrow], 16 keys per MFMA (16x16x16). The
     // score tile's output layout (lane (q, group g) holds keys 4g..4g+3) is exactly the B operand
     // layout, so the probabilities feed the MFMA without a shuffle; the A operand holds
-    // V[keys 4g..4g+3][d] for d = dt*16 + col.
+    // V[keys 4g..4g+3][d] for d = col * DT + dt.
 #pragma unroll
     for (int kt = 0; kt < KT; ++kt) {
       s4_t pop[NQ];
@@ -609,13 +618,15 @@ void attention_kernel(const AttentionArgs a) {
         pop[nq] = __builtin_bit_cast(s4_t, u32x2{pack_bf16x2(pv[0], pv[1]), pack_bf16x2(pv[2], pv[3])});
       }
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        const u32x2 vv = {v_element(vst, kt, 0, dt) | (v_element(vst, kt, 1, dt) << 16),
-                          v_element(vst, kt, 2, dt) | (v_element(vst, kt, 3, dt) << 16)};
+      for (int b = 0; b < kVBlocks; ++b) {
+        u32x2 pairs[8];
+        v_block(vst, b, pairs);
 #pragma unroll
-        for (int nq = 0; nq < NQ; ++nq)
-          o[nq][dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s4_t, vv), pop[nq],
-                                                                o[nq][dt], 0, 0, 0);
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+          for (int nq = 0; nq < NQ; ++nq)
+            o[nq][8 * b + j] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
+                __builtin_bit_cast(s4_t, pairs[j]), pop[nq], o[nq][8 * b + j], 0, 0, 0);
       }
     }
   };
@@ -662,7 +673,7 @@ void attention_kernel(const AttentionArgs a) {
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
       for (int e = 0; e < 4; ++e)
-        co[(static_cast<size_t>(wave) * NQ * 16 + qr) * D + dt * 16 + group * 4 + e] = o[nq][dt][e];
+        co[(static_cast<size_t>(wave) * NQ * 16 + qr) * D + (group * 4 + e) * DT + dt] = o[nq][dt][e];
   }
   __syncthreads();
 
