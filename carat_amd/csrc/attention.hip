@@ -49,6 +49,23 @@ __device__ __forceinline__ u32x4 e4m3x8_to_bf16x8(u32x2 raw) {
                e4m3x2_to_bf16x2<false>(raw.y), e4m3x2_to_bf16x2<true>(raw.y)};
 }
 
+// Max / sum over the four lane groups of a column (lanes l, l^16, l^32, l^48) with gfx950's
+// cross-row lane swaps: VALU only, no LDS round trip. Each step combines the same two values in
+// every lane that holds them (the swap returns them in either order; max and + commute), so the
+// result is the one the xor-shuffle reduction gives, bit for bit.
+__device__ __forceinline__ float groups_max(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float groups_sum(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 struct KeyRange {
   int lo;
   int hi;  // inclusive
@@ -574,8 +591,7 @@ void attention_kernel(const AttentionArgs a) {
             block_max = fmaxf(block_max, v);
           }
       }
-      block_max = fmaxf(block_max, __shfl_xor(block_max, 16, kWave));
-      block_max = fmaxf(block_max, __shfl_xor(block_max, 32, kWave));
+      block_max = groups_max(block_max);
       // The reference max m_run only moves when the column's max grew by more than 2^8: the
       // probabilities are then at most 256 (exact relative rounding in bf16, no fp32 overflow)
       // and the accumulators, which live in AGPRs, are rescaled rarely. exp2(-inf) = 0 covers
@@ -593,8 +609,7 @@ void attention_kernel(const AttentionArgs a) {
           sc[nq][kt][e] = pe;
           local_sum += pe;
         }
-      local_sum += __shfl_xor(local_sum, 16, kWave);
-      local_sum += __shfl_xor(local_sum, 32, kWave);
+      local_sum = groups_sum(local_sum);
       l_run[nq] = l_run[nq] * alpha + local_sum;
       m_run[nq] = m_new;
       if (__builtin_amdgcn_ballot_w64(grow) != 0) {
@@ -1038,8 +1053,7 @@ void attention_dsplit_kernel(const AttentionArgs a) {
         sc[nt][e] = v;
         block_max = fmaxf(block_max, v);
       }
-      block_max = fmaxf(block_max, __shfl_xor(block_max, 16, kWave));
-      block_max = fmaxf(block_max, __shfl_xor(block_max, 32, kWave));
+      block_max = groups_max(block_max);
       const bool grow = block_max > m_run[nt] + 8.0f;
       const float m_new = grow ? block_max : m_run[nt];
       const float m_use = m_new == -INFINITY ? 0.0f : m_new;
@@ -1051,8 +1065,7 @@ void attention_dsplit_kernel(const AttentionArgs a) {
         sc[nt][e] = pe;
         local_sum += pe;
       }
-      local_sum += __shfl_xor(local_sum, 16, kWave);
-      local_sum += __shfl_xor(local_sum, 32, kWave);
+      local_sum = groups_sum(local_sum);
       l_run[nt] = l_run[nt] * alpha + local_sum;
       m_run[nt] = m_new;
       if (__builtin_amdgcn_ballot_w64(grow) != 0) {
