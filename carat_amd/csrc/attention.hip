@@ -288,7 +288,10 @@ void attention_kernel(const AttentionArgs a) {
   constexpr int kStageCap = kFp8 ? 6 : 4;
   constexpr int kStages = kStagesFit > kStageCap ? kStageCap : (kStagesFit < 1 ? 1 : kStagesFit);
   constexpr int kWaveBytes = kStages * kStageBytes;
-  constexpr int kCombineBytes = (2 * kWaves * NQ * 16 + kWaves * NQ * 16 * D) * 4;
+  // wave merge: m and l per (wave, query row), then the O rows at a padded stride (no bank
+  // conflicts between the rows of one store)
+  constexpr int kCoStride = D + 4;
+  constexpr int kCombineBytes = (2 * kWaves * NQ * 16 + kWaves * NQ * 16 * kCoStride) * 4;
   constexpr int kLoopBytes = kWaves * kWaveBytes + kQBytes;  // V stages, then Q (kQInLds)
   // the fused QKV post-processing's query rows [16][D] bf16 sit past the stages
   constexpr int kQTileBytes = kFuseSplits > 0 ? 16 * D * 2 : 0;
@@ -676,7 +679,7 @@ void attention_kernel(const AttentionArgs a) {
   __syncthreads();
   float *cm = reinterpret_cast<float *>(lds);                // [wave][NQ*16]
   float *cl = cm + kWaves * NQ * 16;                         // [wave][NQ*16]
-  float *co = cl + kWaves * NQ * 16;                         // [wave][NQ*16][D]
+  float *co = cl + kWaves * NQ * 16;                         // [wave][NQ*16][kCoStride]
 #pragma unroll
   for (int nq = 0; nq < NQ; ++nq) {
     const int qr = nq * 16 + col;
@@ -684,15 +687,21 @@ void attention_kernel(const AttentionArgs a) {
       cm[wave * NQ * 16 + qr] = m_run[nq];
       cl[wave * NQ * 16 + qr] = l_run[nq];
     }
+    // row 4g + e of every output tile: d = (4g + e) * DT + dt, DT contiguous floats
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
+    for (int e = 0; e < 4; ++e) {
+      float *dst = co + (static_cast<size_t>(wave) * NQ * 16 + qr) * kCoStride + (group * 4 + e) * DT;
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        co[(static_cast<size_t>(wave) * NQ * 16 + qr) * D + (group * 4 + e) * DT + dt] = o[nq][dt][e];
+      for (int dt = 0; dt < DT; dt += 4)
+        *reinterpret_cast<v4f *>(dst + dt) =
+            v4f{o[nq][dt][e], o[nq][dt + 1][e], o[nq][dt + 2][e], o[nq][dt + 3][e]};
+    }
   }
   __syncthreads();
 
-  // Thread-per-(query row, d) combine; `lr` is the workgroup's row, qr = q0 + lr the item's.
+  // One thread per (query row, 8 consecutive d): the row's wave factors once, then 8 outputs in
+  // the same arithmetic order per element as ever; `lr` is the workgroup's row, qr = q0 + lr the
+  // item's.
   const int rows_total = qtiles * NQ * 16;
   const bool single = n_chunks == 1;
   float *part = nullptr;
@@ -702,33 +711,54 @@ void attention_kernel(const AttentionArgs a) {
   }
   const int local_rows = min(NQ * 16, qrows - q0);
   float amax = 0.0f;
-  for (int idx = threadIdx.x; idx < local_rows * D; idx += kThreads) {
-    const int lr = idx / D;
+  constexpr int kGroups8 = D / 8;
+  for (int idx = threadIdx.x; idx < local_rows * kGroups8; idx += kThreads) {
+    const int lr = idx / kGroups8;
     const int qr = q0 + lr;
-    const int d = idx % D;
+    const int d0 = (idx % kGroups8) * 8;
     float m = -INFINITY;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) m = fmaxf(m, cm[w * NQ * 16 + lr]);
-    float l = 0.0f, acc = 0.0f;
+    float l = 0.0f, acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     if (m != -INFINITY) {
 #pragma unroll
       for (int w = 0; w < kWaves; ++w) {
         const float f = exp2f(cm[w * NQ * 16 + lr] - m);
         l += f * cl[w * NQ * 16 + lr];
-        acc += f * co[(static_cast<size_t>(w) * NQ * 16 + lr) * D + d];
+        const float *src = co + (static_cast<size_t>(w) * NQ * 16 + lr) * kCoStride + d0;
+        const v4f lo = *reinterpret_cast<const v4f *>(src);
+        const v4f hi = *reinterpret_cast<const v4f *>(src + 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          acc[e] += f * lo[e];
+          acc[4 + e] += f * hi[e];
+        }
       }
     }
     if (single) {
       const int local_head = qr / T;
       const int t = qr % T;
-      float value = l > 0.0f ? acc / l : 0.0f;
-      if constexpr (kFp8) value *= a.v_scale;
-      const bf16_t hv = f32_to_bf16(value);
-      a.out[((static_cast<size_t>(r) * T + t) * a.query_heads + h * G + local_head) * D + d] = hv;
-      amax = fmaxf(amax, fabsf(bf16_to_f32(hv)));
+      uint32_t packed[4];
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        float v0 = l > 0.0f ? acc[e] / l : 0.0f;
+        float v1 = l > 0.0f ? acc[e + 1] / l : 0.0f;
+        if constexpr (kFp8) {
+          v0 *= a.v_scale;
+          v1 *= a.v_scale;
+        }
+        const bf16_t h0 = f32_to_bf16(v0), h1 = f32_to_bf16(v1);
+        amax = fmaxf(amax, fmaxf(fabsf(bf16_to_f32(h0)), fabsf(bf16_to_f32(h1))));
+        packed[e / 2] = static_cast<uint32_t>(h0) | (static_cast<uint32_t>(h1) << 16);
+      }
+      *reinterpret_cast<u32x4 *>(
+          a.out + ((static_cast<size_t>(r) * T + t) * a.query_heads + h * G + local_head) * D + d0) =
+          u32x4{packed[0], packed[1], packed[2], packed[3]};
     } else {
-      part[static_cast<size_t>(qr) * (D + 2) + d] = acc;
-      if (d == 0) {
+      float *dst = part + static_cast<size_t>(qr) * (D + 2) + d0;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dst[e] = acc[e];
+      if (d0 == 0) {
         part[static_cast<size_t>(qr) * (D + 2) + D] = m;
         part[static_cast<size_t>(qr) * (D + 2) + D + 1] = l;
       }
