@@ -444,6 +444,9 @@ void attention_kernel(const AttentionArgs a) {
     static_assert(NQ == 1 && !kQInLds && !kFp8, "fused QKV shape");
     // the query rows [qr = local_head * T + t][D] bf16, in LDS of their own
     bf16_t *q_tile = reinterpret_cast<bf16_t *>(lds + kLdsBytes - kQTileBytes);
+    // the prologue's loads went out before the early stages: waiting for them leaves the stages
+    // in flight
+    wait_vmcnt<kEarlyStages * kLoadsPerStage>();
     fused.finish(a, r, h, p, slot, q_tile, chunk == 0);
     if (kv_async) {
       wait_lgkmcnt0();  // the query rows are in LDS (the K/V stores stay in flight)
