@@ -30,12 +30,14 @@ struct WeightLayout {
   int n = 0;               // feature rows
   int row_bytes = 0;       // bytes per row (K for e4m3, 2K for bf16); multiple of 128
   int tiles_per_wave = 1;  // F: 1, 2 or 4 (even for gate/up)
-  int waves = 4;           // W: waves per workgroup, 3 or 4
+  int waves = 4;           // W: waves per workgroup, 3 or 4 (1 or 2 for few-row weights)
   bool gate_up = false;
 };
 
 // Storage layout for an [n][row_bytes] weight: the widest F that still leaves >= 64 workgroups.
-WeightLayout gemm_weight_layout(int n, int row_bytes, bool gate_up);
+// few_rows: the weight serves GEMMs of a few rows per call (the assistant's), which are latency-
+// bound; a small grid then takes narrower workgroups (1 or 2 waves).
+WeightLayout gemm_weight_layout(int n, int row_bytes, bool gate_up, bool few_rows = false);
 int gemm_blocks_n(const WeightLayout &layout);
 void pack_weight(const void *row_major, void *packed, const WeightLayout &layout,
                  hipStream_t stream);

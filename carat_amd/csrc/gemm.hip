@@ -89,7 +89,7 @@ __global__ __launch_bounds__(256) void pack_weight_kernel(const unsigned char *s
 void check_layout(const WeightLayout &l) {
   const int f = l.tiles_per_wave;
   if (l.n <= 0 || l.row_bytes <= 0 || l.row_bytes % kStepBytes != 0 ||
-      (f != 1 && f != 2 && f != 4) || (l.gate_up && f == 1) || (l.waves != 3 && l.waves != 4) ||
+      (f != 1 && f != 2 && f != 4) || (l.gate_up && f == 1) || l.waves < 1 || l.waves > 4 ||
       l.n % (16 * l.waves * f) != 0)
     throw std::runtime_error("invalid packed weight layout");
 }
@@ -684,6 +684,9 @@ template <int F> constexpr int kStages = F == 1 ? 4 : 3;
 template <bool kFp8, GemmEpilogue kEpi, int TT, int kS>
 void launch_tiles(const GemmArgs &a, bool many, bool group4, dim3 grid, hipStream_t stream) {
   const int w = a.w_layout.waves;
+  // one- and two-wave layouts (few-row weights) are built for one 32-row token block only
+  if ((w == 1 || w == 2) && !(TT == 2 && kS == 0))
+    throw std::runtime_error("a few-row weight layout serves at most 32 rows per call");
   // Many token blocks (prefill steps): the weights mostly come from L2, and two workgroups per CU
   // (two weight stages, <= 256 registers) keep the MFMAs fed while one of them waits.
   switch (a.w_layout.tiles_per_wave) {
@@ -697,12 +700,20 @@ void launch_tiles(const GemmArgs &a, bool many, bool group4, dim3 grid, hipStrea
           return;
         }
       }
+      if constexpr (TT == 2 && kS == 0) {  // few-row layouts (gemm_weight_layout few_rows)
+        if (w == 1) { gemm_kernel<kFp8, kEpi, TT, 1, 1, kStages<1>, 1, 1, kS><<<grid, 64, 0, stream>>>(a); return; }
+        if (w == 2) { gemm_kernel<kFp8, kEpi, TT, 1, 2, kStages<1>, 1, 1, kS><<<grid, 128, 0, stream>>>(a); return; }
+      }
       if (w == 3) gemm_kernel<kFp8, kEpi, TT, 1, 3, kStages<1>, 1, 1, kS><<<grid, 192, 0, stream>>>(a);
       else gemm_kernel<kFp8, kEpi, TT, 1, 4, kStages<1>, 1, 1, kS><<<grid, 256, 0, stream>>>(a);
       return;
     }
     break;
   case 2:
+    if constexpr (TT == 2 && kS == 0) {
+      if (w == 1) { gemm_kernel<kFp8, kEpi, TT, 2, 1, kStages<2>, 1, 1, kS><<<grid, 64, 0, stream>>>(a); return; }
+      if (w == 2) { gemm_kernel<kFp8, kEpi, TT, 2, 2, kStages<2>, 1, 1, kS><<<grid, 128, 0, stream>>>(a); return; }
+    }
     if (w == 3) gemm_kernel<kFp8, kEpi, TT, 2, 3, kStages<2>, 1, 1, kS><<<grid, 192, 0, stream>>>(a);
     else gemm_kernel<kFp8, kEpi, TT, 2, 4, kStages<2>, 1, 1, kS><<<grid, 256, 0, stream>>>(a);
     return;
@@ -835,7 +846,7 @@ void launch_gemm(const GemmArgs &a, hipStream_t stream) {
 
 }  // namespace
 
-WeightLayout gemm_weight_layout(int n, int row_bytes, bool gate_up) {
+WeightLayout gemm_weight_layout(int n, int row_bytes, bool gate_up, bool few_rows) {
   // The widest F (longest contiguous run per workgroup step) that still leaves >= 128
   // workgroups; measured on MI355X for the verify shapes (qkv 8192 and o/down 5376 rows take
   // F = 1, gate/up 43008 and the lm_head take F = 4). Gate/up weights feed the GELU epilogue,
@@ -865,6 +876,25 @@ WeightLayout gemm_weight_layout(int n, int row_bytes, bool gate_up) {
     const int wg4 = (n / 64) * gemm_choose_splits(n / 64, steps);
     const int wg3 = (n / 48) * gemm_choose_splits(n / 48, steps);
     if (wg4 < 200 && wg3 > wg4 && wg3 <= 256) l.waves = 3;
+  }
+  // GEMMs of a few rows per call (the assistant's draft step, 24 rows) are latency-bound: when
+  // the grid stays small, narrower workgroups (fewer waves, the same F) give more of them -- the
+  // widest that reaches 240 workgroups with its split-K factor, else one wave.
+  if (few_rows) {
+    const int steps = row_bytes / 128;
+    auto workgroups = [&](int w) {
+      const int blocks = n / (16 * w * l.tiles_per_wave);
+      return gate_up ? blocks : blocks * gemm_choose_splits(blocks, steps);
+    };
+    if (workgroups(l.waves) < 240) {
+      int pick = 1;
+      for (int w = l.waves - 1; w >= 1; --w)
+        if (n % (16 * w * l.tiles_per_wave) == 0 && workgroups(w) >= 240) {
+          pick = w;
+          break;
+        }
+      if (n % (16 * pick * l.tiles_per_wave) == 0) l.waves = pick;
+    }
   }
   check_layout(l);
   return l;

@@ -446,8 +446,8 @@ struct BatchModelRunner::Implementation {
     return staging.get();
   }
 
-  void pack_from_staging(PackedWeight &w, int n, int row_bytes, bool gate_up) {
-    w.layout = gemm_weight_layout(n, row_bytes, gate_up);
+  void pack_from_staging(PackedWeight &w, int n, int row_bytes, bool gate_up, bool few_rows = false) {
+    w.layout = gemm_weight_layout(n, row_bytes, gate_up, few_rows);
     w.data.allocate(static_cast<size_t>(n) * row_bytes);
     pack_weight(staging.get(), w.data.get(), w.layout, stream);
   }
@@ -514,7 +514,9 @@ struct BatchModelRunner::Implementation {
       upload_segment(segment, dst, count * sizeof(bf16_t));
     else
       fill_normal_bf16(static_cast<bf16_t *>(dst), count, seed_for(tensor), 0.0f, stddev, stream);
-    pack_from_staging(w, n, 2 * k, gate_up);
+    // the assistant's projections run a draft step's rows (<= the batch) per call
+    const bool few_rows = batch_size <= 32;
+    pack_from_staging(w, n, 2 * k, gate_up, few_rows);
     if (fp8 == nullptr) return;
     if (load_staging.bytes() < count) {
       hip_check(hipStreamSynchronize(stream), "synchronise before staging growth");
@@ -528,7 +530,7 @@ struct BatchModelRunner::Implementation {
       quantize_weight_bf16_to_fp8(static_cast<const bf16_t *>(dst), e4m3, count, fp8_scale,
                                   init_scratch.as<float>(), stream);
     }
-    fp8->layout = gemm_weight_layout(n, k, gate_up);
+    fp8->layout = gemm_weight_layout(n, k, gate_up, few_rows);
     fp8->data.allocate(count);
     pack_weight(e4m3, fp8->data.get(), fp8->layout, stream);
   }
