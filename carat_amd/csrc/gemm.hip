@@ -4,11 +4,11 @@
 // Every weight byte is used by exactly one wave, so weights stream HBM -> VGPRs directly, P steps
 // ahead, from the packed layout (gemm.h) in which a workgroup's weights for one K step are one
 // contiguous run and each wave load instruction reads 1 KiB contiguous. The activations are
-// gathered from their row-major bf16 producer output by DMA and, for e4m3 weights, quantised in
-// LDS (see gemm_kernel): no separate preparation kernel. The activations are shared by all waves of a workgroup: a prologue kernel lays them out
-// once in MFMA-operand order (and, for fp8, quantises them with the producer's per-tensor amax:
-// scale = amax / 448, q = e4m3(x * (1 / scale)), cuda/linear.cu:107-110,143-186), and each step's
-// activation tile is DMA'd global -> LDS (global_load_lds_dwordx4). Loads are issued branch-free
+// shared by all waves of a workgroup and stay row-major: bf16 GEMMs read their producer's output;
+// for e4m3 weights they are quantised once with the producer's per-tensor amax (scale =
+// amax / 448, q = e4m3(x * (1 / scale)), cuda/linear.cu:107-110,143-186) by prepare_x_kernel or
+// by the producing row kernel itself. Each step's 128-byte slice of every token row is DMA'd
+// global -> LDS (global_load_lds_dwordx4). Loads are issued branch-free
 // (tail steps re-issue the last step's addresses, which hit in cache) so the in-order vmcnt counter
 // keeps P steps in flight.
 //
@@ -111,50 +111,45 @@ void launch_pack(const void *src, void *dst, const WeightLayout &l, bool pack, h
 }
 
 // ---------------------------------------------------------------------------------------------
-// e4m3 activation operand: out[m_block][step][tile][half][lane][16 B], lane = group*16 + col:
-// token = tile*16 + col, K bytes [half*64 + group*16, +16) of the step, quantised with the
-// producer's per-tensor scale amax / 448 (cuda/linear.cu:107-110, 143-186). Quantising once here
-// keeps the per-workgroup operand traffic of the GEMM at one byte per element.
+// e4m3 activation operand: out[token][k], row-major like the bf16 producer output, quantised with
+// the producer's per-tensor scale amax / 448 (cuda/linear.cu:107-110, 143-186). Quantising once
+// here keeps the per-workgroup operand traffic of the GEMM at one byte per element; the GEMM
+// gathers each token's 128-byte step slice (one cache line) by DMA, as it gathers bf16 rows, and
+// a producer that owns a token row writes whole lines of it.
 // ---------------------------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void prepare_x_kernel(const bf16_t *x, int ldx, int m, int k,
                                                         const float *x_amax, int amax_stripes,
                                                         int token_tiles, unsigned char *out) {
-  const int steps = k / kStepBytes;
+  const int pieces = k / 16;  // 16-byte output chunks per token
   const int chunk = blockIdx.x * blockDim.x + threadIdx.x;  // one 16-byte chunk per thread
-  const int chunks_per_block = steps * token_tiles * 128;
-  const int m_block = blockIdx.y;
-  const int lane = chunk & 63;
-  const int half = (chunk >> 6) & 1;
-  const int tile = (chunk >> 7) % token_tiles;
-  const int step = (chunk >> 7) / token_tiles;
-  const int token = m_block * token_tiles * 16 + tile * 16 + (lane & 15);
-  const int group = lane >> 4;
+  const int tokens = token_tiles * 16;
+  const int token = blockIdx.y * tokens + chunk / pieces;
+  const int piece = chunk % pieces;
   // The row slice goes out before the amax: neither load waits for the other. Lanes past the
-  // chunks or tokens re-read a valid slice (token m - 1) and store nothing or zeros.
-  const bf16_t *src = x + static_cast<size_t>(min(token, m - 1)) * ldx + step * 128 + half * 64 + group * 16;
+  // tokens re-read a valid slice (token m - 1) and store nothing.
+  const bf16_t *src = x + static_cast<size_t>(min(token, m - 1)) * ldx + piece * 16;
   const u32x4 lo = *reinterpret_cast<const u32x4 *>(src);
   const u32x4 hi = *reinterpret_cast<const u32x4 *>(src + 8);
   const float inv = 1.0f / fp8_scale_from_amax(amax_read(x_amax, amax_stripes));
-  if (chunk >= chunks_per_block) return;
-  u32x4 value = {0u, 0u, 0u, 0u};
-  if (token < m) {
-    const uint32_t w[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+  if (chunk >= tokens * pieces || token >= m) return;
+  u32x4 value;
+  const uint32_t w[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
-      value[q] = f32x4_to_e4m3x4(__uint_as_float(w[2 * q] << 16) * inv,
-                                 __uint_as_float(w[2 * q] & 0xffff0000u) * inv,
-                                 __uint_as_float(w[2 * q + 1] << 16) * inv,
-                                 __uint_as_float(w[2 * q + 1] & 0xffff0000u) * inv);
-  }
-  reinterpret_cast<u32x4 *>(out)[static_cast<size_t>(m_block) * chunks_per_block + chunk] = value;
+  for (int q = 0; q < 4; ++q)
+    value[q] = f32x4_to_e4m3x4(__uint_as_float(w[2 * q] << 16) * inv,
+                               __uint_as_float(w[2 * q] & 0xffff0000u) * inv,
+                               __uint_as_float(w[2 * q + 1] << 16) * inv,
+                               __uint_as_float(w[2 * q + 1] & 0xffff0000u) * inv);
+  reinterpret_cast<u32x4 *>(out + static_cast<size_t>(token) * k)[piece] = value;
 }
 
 // Fp8Scaling::channel / ::block_128 activation operands (quantize_bf16_rows_kernel and
 // quantize_activation_block_128_kernel, cuda/linear.cu:300-316, 382-401): scale =
 // max(amax / 448, 2^-24) per token row (channel) or per token and 128-element K step (block_128),
-// q = e4m3(x / scale), written in the operand layout of prepare_x_kernel. Scales: channel
-// x_scales[token]; block_128 x_scales[m_block][step][col][token tile] (token = tile * 16 + col of
-// the block), so that a lane's token tiles of one step are contiguous. Tokens past m get zeros.
+// q = e4m3(x / scale), written in the row-major operand layout of prepare_x_kernel. Scales:
+// channel x_scales[token]; block_128 x_scales[m_block][step][col][token tile] (token = tile * 16 +
+// col of the block), so that a lane's token tiles of one step are contiguous. Tokens past m get a
+// scale but no operand row (the GEMM re-reads row m - 1 for them and stores nothing).
 __device__ __forceinline__ u32x4 quantize_chunk(u32x4 lo, u32x4 hi, float scale, bool live) {
   u32x4 value = {0u, 0u, 0u, 0u};
   if (!live) return value;
@@ -177,15 +172,10 @@ __device__ __forceinline__ float chunk_amax(u32x4 lo, u32x4 hi) {
   return m;
 }
 
-// channel: one workgroup per token of the padded token blocks
+// channel: one workgroup per token of the padded token blocks (scales for all, rows for live ones)
 __global__ __launch_bounds__(256) void prepare_x_rows_kernel(const bf16_t *x, int ldx, int m, int k,
-                                                             int token_tiles, unsigned char *out,
-                                                             float *x_scales) {
+                                                             unsigned char *out, float *x_scales) {
   const int token = blockIdx.x;
-  const int steps = k / kStepBytes;
-  const int m_block = token / (token_tiles * 16);
-  const int tile = (token / 16) % token_tiles;
-  const int col = token % 16;
   const bool live = token < m;
   const bf16_t *src = x + static_cast<size_t>(min(token, m - 1)) * ldx;
   const int chunks = k / 16;
@@ -201,12 +191,9 @@ __global__ __launch_bounds__(256) void prepare_x_rows_kernel(const bf16_t *x, in
   const float scale = fmaxf(amax / 448.0f, 0x1p-24f);
   if (threadIdx.x == 0) x_scales[token] = scale;
   for (int c = threadIdx.x; c < chunks; c += 256) {
-    const int step = c / 8, half = (c / 4) % 2, group = c % 4;
     const u32x4 value = quantize_chunk(*reinterpret_cast<const u32x4 *>(src + c * 16),
                                        *reinterpret_cast<const u32x4 *>(src + c * 16 + 8), scale, live);
-    const size_t chunk = ((static_cast<size_t>(m_block) * steps + step) * token_tiles + tile) * 128 +
-                         half * 64 + group * 16 + col;
-    reinterpret_cast<u32x4 *>(out)[chunk] = value;
+    if (live) reinterpret_cast<u32x4 *>(out + static_cast<size_t>(token) * k)[c] = value;
   }
 }
 
@@ -231,10 +218,11 @@ __global__ __launch_bounds__(256) void prepare_x_blocks_kernel(const bf16_t *x, 
   amax = fmaxf(amax, __shfl_xor(amax, 32, kWave));
   const float scale = fmaxf(amax / 448.0f, 0x1p-24f);
   const bool live = token < m;
-  u32x4 *dst = reinterpret_cast<u32x4 *>(out) +
-               ((static_cast<size_t>(m_block) * steps + step) * token_tiles + tile) * 128 + lane;
-  dst[0] = quantize_chunk(lo0, hi0, scale, live);
-  dst[64] = quantize_chunk(lo1, hi1, scale, live);
+  if (live) {
+    u32x4 *dst = reinterpret_cast<u32x4 *>(out + static_cast<size_t>(token) * k + step * 128) + group;
+    dst[0] = quantize_chunk(lo0, hi0, scale, true);
+    dst[4] = quantize_chunk(lo1, hi1, scale, true);
+  }
   if (group == 0)
     x_scales[((static_cast<size_t>(m_block) * steps + step) * 16 + col) * token_tiles + tile] = scale;
 }
@@ -259,11 +247,12 @@ void gemm_kernel(const GemmArgs a) {
   static_assert(kScale == 0 || kFp8, "scaled operands are e4m3");
   constexpr int FL = F / kBlocks;  // tiles per wave in the packed layout
   // Activation operand, one LDS stage per K step, filled by DMA (global_load_lds_dwordx4):
-  //  - e4m3 weights: the prepared operand (prepare_x_kernel), already in MFMA order, 1 B/element;
-  //  - bf16 weights: gathered straight from the row-major bf16 X: the 128-byte slice of every
-  //    token row that matches the weight step, its 16-byte chunks XOR-swizzled by the row index
-  //    (chunk c of row t at position c ^ (t mod 8)), so one chunk of 16 consecutive rows spreads
-  //    over distinct banks; the B operand is read from there directly.
+  //  - e4m3 weights: the prepared row-major operand (prepare_x_kernel), 1 B/element;
+  //  - bf16 weights: the row-major bf16 X itself;
+  //  either way the 128-byte slice of every token row that matches the weight step, its 16-byte
+  //  chunks XOR-swizzled by the row index (chunk c of row t at position c ^ (t mod 8)), so one
+  //  chunk of 16 consecutive rows spreads over distinct banks; the B operand is read from there
+  //  directly.
   constexpr int kXRowBytes = 128;
   constexpr int kXChunks = kXRowBytes / 16;
   constexpr int kXStage = TT * 16 * kXRowBytes;   // = TT * kTileBytes for both operand kinds
@@ -328,23 +317,21 @@ void gemm_kernel(const GemmArgs a) {
     if constexpr (kEpi == GemmEpilogue::gelu_gate) return f < F / 2 ? feature0[f] : a.n / 2 + feature0[f];
     else return feature0[f];
   };
-  // This thread's DMA sources for stage chunk id = unit(i) * 64 + lane. e4m3: the
-  // prepared operand, linear. bf16: row id / 8 of X at swizzled position id % 8 (rows past M
-  // re-read row M - 1; their outputs are never stored).
+  // This thread's DMA sources for stage chunk id = unit(i) * 64 + lane: row id / 8 of the
+  // row-major activations (bf16 X, or the prepared e4m3 operand) at swizzled position id % 8
+  // (rows past M re-read row M - 1; their outputs are never stored).
   auto xunit = [&](int i) { return min(i * W + wave, kXUnits - 1); };
   const unsigned char *xsrc[kXDma];
 #pragma unroll
   for (int i = 0; i < kXDma; ++i) {
     const int id = xunit(i) * 64 + lane;
-    if constexpr (kFp8) {
-      xsrc[i] = a.xprep + (static_cast<size_t>(m_block) * total_steps + step0) * kXStage + id * 16;
-    } else {
-      const int row = id / kXChunks;
-      const int chunk = (id % kXChunks) ^ (row % kXChunks);
-      const int token = min(m_block * TT * 16 + row, a.m - 1);
-      xsrc[i] = reinterpret_cast<const unsigned char *>(a.x + static_cast<size_t>(token) * a.ldx) +
-                static_cast<size_t>(step0) * kXRowBytes + chunk * 16;
-    }
+    const int row = id / kXChunks;
+    const int chunk = (id % kXChunks) ^ (row % kXChunks);
+    const int token = min(m_block * TT * 16 + row, a.m - 1);
+    const unsigned char *row_base =
+        kFp8 ? a.xprep + static_cast<size_t>(token) * row_bytes
+             : reinterpret_cast<const unsigned char *>(a.x + static_cast<size_t>(token) * a.ldx);
+    xsrc[i] = row_base + static_cast<size_t>(step0) * kXRowBytes + chunk * 16;
   }
 
   u32x4 wreg[P][F][2];
@@ -373,7 +360,7 @@ void gemm_kernel(const GemmArgs a) {
 #pragma unroll
     for (int i = 0; i < kXDma; ++i)
       __builtin_amdgcn_global_load_lds(
-          reinterpret_cast<const void *>(xsrc[i] + static_cast<size_t>(s) * (kFp8 ? kXStage : kXRowBytes)),
+          reinterpret_cast<const void *>(xsrc[i] + static_cast<size_t>(s) * kXRowBytes),
           reinterpret_cast<void __attribute__((address_space(3))) *>(
               reinterpret_cast<uintptr_t>(stage + xunit(i) * 1024)),
           16, 0, 0);
@@ -424,16 +411,12 @@ void gemm_kernel(const GemmArgs a) {
 
   // Token tile j+1's B operand is read from LDS while tile j's MFMAs run (the scheduling
   // barriers keep the compiler from sinking the reads next to their use).
-  // B operand of token tile j, half h: e4m3 from the prepared stage ([tile][half][lane][16 B]);
-  // bf16 from the swizzled stage (row j*16+col, chunk h*4+group of the 128-byte row slice).
+  // B operand of token tile j, half h, from the swizzled stage (row j*16+col, chunk h*4+group
+  // of the 128-byte row slice).
   auto b_operand = [&](int slot, int j, int h) -> u32x4 {
-    if constexpr (kFp8) {
-      return *reinterpret_cast<const u32x4 *>(lds + slot * kXStage + j * kTileBytes + h * 1024 + lane * 16);
-    } else {
-      const int row = j * 16 + col;
-      const int chunk = (h * 4 + group) ^ (row % kXChunks);
-      return *reinterpret_cast<const u32x4 *>(lds + slot * kXStage + row * kXRowBytes + chunk * 16);
-    }
+    const int row = j * 16 + col;
+    const int chunk = (h * 4 + group) ^ (row % kXChunks);
+    return *reinterpret_cast<const u32x4 *>(lds + slot * kXStage + row * kXRowBytes + chunk * 16);
   };
 
   // block_128: one step's product of weight tile f and token tile j, unscaled (a fresh
@@ -798,7 +781,7 @@ void launch_gemm(const GemmArgs &a, hipStream_t stream) {
     if (a.scaling == 1) {
       if (static_cast<size_t>(m_blocks) * tokens_per_block > a.x_scales_capacity)
         throw std::runtime_error("GEMM activation scale workspace too small");
-      prepare_x_rows_kernel<<<m_blocks * tokens_per_block, 256, 0, stream>>>(a.x, a.ldx, a.m, a.k, tt,
+      prepare_x_rows_kernel<<<m_blocks * tokens_per_block, 256, 0, stream>>>(a.x, a.ldx, a.m, a.k,
                                                                             a.xprep, a.x_scales);
     } else if (a.scaling == 2) {
       if (static_cast<size_t>(m_blocks) * total_steps * tokens_per_block > a.x_scales_capacity)
@@ -808,7 +791,7 @@ void launch_gemm(const GemmArgs &a, hipStream_t stream) {
       prepare_x_blocks_kernel<<<waves_grid, 256, 0, stream>>>(a.x, a.ldx, a.m, a.k, tt, a.xprep,
                                                              a.x_scales);
     } else if (!a.xprep_ready) {
-      prepare_x_kernel<<<grid, 256, 0, stream>>>(a.x, a.ldx, a.m, a.k, a.x_amax, a.amax_stripes, tt,
+prepare_x_kernel<<<grid, 256, 0, stream>>>(a.x, a.ldx, a.m, a.k, a.x_amax, a.amax_stripes, tt,
                                                a.xprep);
     }
   }

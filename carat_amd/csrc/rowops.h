@@ -47,12 +47,11 @@ struct RowArgs {
   int amax_stripes = 1;            // floats per amax (x_amax and y_amax), see amax_publish
   // Optional (the verify step's layer-end rows, <= kFusedQuantizeRows rows): y also goes out
   // quantised to e4m3 with its per-tensor scale (amax / 448), in the fp8 GEMM's activation
-  // operand order (gemm.hip prepare_x_kernel's layout, xprep_token_tiles tiles per token block),
+  // operand layout (gemm.hip prepare_x_kernel's: row-major e4m3),
   // so no separate quantisation kernel runs. The workgroups agree on the amax through `sync`
   // (kFusedSyncWords zeroed words, kAmaxStripeFloats floats apart: arrival counters and the
   // released amax); a wait that exceeds its bound sets *fault and the output is not to be used.
   unsigned char *xprep = nullptr;
-  int xprep_token_tiles = 8;
   unsigned *sync = nullptr;
   int32_t *fault = nullptr;
   int quantize_spins = kFusedQuantizeSpins;  // bound of a wait for the agreed amax (0: no wait)
@@ -62,7 +61,7 @@ void launch_row_kernel(const RowArgs &args, hipStream_t stream);
 // Whether launch_row_kernel can quantise `args`'s output into the operand workspace (the
 // layer-end shape: split-K partials of an fp8 GEMM with 1-4 or 8 splits, both norms, a width
 // with a layer-end instance that is a multiple of 128, <= kFusedQuantizeRows rows, the output
-// amax, 2 or 8 token tiles). The xprep, sync and fault fields are not looked at.
+// amax). The xprep, sync and fault fields are not looked at.
 bool row_kernel_can_fuse_quantization(const RowArgs &args);
 
 // ---------------------------------------------------------------------------------------------

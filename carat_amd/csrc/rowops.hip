@@ -186,9 +186,13 @@ __global__ __launch_bounds__(kThreads) void layer_end_kernel(const RowArgs a) {
   }
 
   // stage 1: r1 = bf16(norm(v) * w1 + residual) [* scalar]
+  // With the fused quantisation every store waits until the workgroups have agreed on the amax, so
+  // that the agreement's release finds no store of this kernel to write back.
+  const bool fused = a.xprep != nullptr && a.y_amax != nullptr;
   const bool has_scalar = a.scalar != nullptr;
   float inv = inverse_rms(block_sum(square_sum, scratch), a.width, a.eps);
   square_sum = 0.0f;
+  f32x4_t r1v[Q];
 #pragma unroll
   for (int i = 0; i < Q; ++i) {
     const int q = threadIdx.x + i * kThreads;
@@ -199,7 +203,8 @@ __global__ __launch_bounds__(kThreads) void layer_end_kernel(const RowArgs a) {
       v[i][c] = q < quads ? r1 : 0.0f;
       square_sum += v[i][c] * v[i][c];
     }
-    if (q < quads) reinterpret_cast<uint2 *>(a.r1_out + row_offset)[q] = f32x4_to_bf16(v[i]);
+    r1v[i] = v[i];
+    if (!fused && q < quads) reinterpret_cast<uint2 *>(a.r1_out + row_offset)[q] = f32x4_to_bf16(v[i]);
   }
 
   // stage 2: y = bf16(norm(r1) * w2), amax
@@ -213,17 +218,17 @@ __global__ __launch_bounds__(kThreads) void layer_end_kernel(const RowArgs a) {
       v[i][c] = round_bf16(v[i][c] * inv * w2[i][c]);  // y, kept for the fused quantisation
       amax = fmaxf(amax, fabsf(v[i][c]));
     }
-    if (q < quads) reinterpret_cast<uint2 *>(a.y_out + row_offset)[q] = f32x4_to_bf16(v[i]);
+    if (!fused && q < quads) reinterpret_cast<uint2 *>(a.y_out + row_offset)[q] = f32x4_to_bf16(v[i]);
   }
   if (a.y_amax == nullptr) return;  // bf16 consumers (the assistant's GEMMs) need no amax
   amax = block_max(amax, scratch);
-  if (a.xprep == nullptr) {
+  if (!fused) {
     if (threadIdx.x == 0) amax_publish(a.y_amax, a.amax_stripes, amax);
     return;
   }
 
   // ---- fused e4m3 quantisation of y: the workgroups agree on the tensor's amax, then each
-  // quantises its own row.
+  // stores r1, y and its row of the quantised operand.
   __shared__ float tensor_amax;
   if (threadIdx.x < kWave) {
     const float total = fused_amax_release(a.y_amax, a.amax_stripes, a.sync, a.fault, gridDim.x, amax,
@@ -232,22 +237,16 @@ __global__ __launch_bounds__(kThreads) void layer_end_kernel(const RowArgs a) {
   }
   __syncthreads();
   const float q_inv = 1.0f / fp8_scale_from_amax(tensor_amax);
-  // operand layout: [m_block][step][tile][half][lane = group * 16 + col][16 B] with token =
-  // m_block * TT * 16 + tile * 16 + col and K bytes [step * 128 + half * 64 + group * 16, +16)
-  const int tt = a.xprep_token_tiles;
-  const int steps = a.width / 128;
-  const int m_block = row / (tt * 16);
-  const int tile = (row / 16) % tt;
-  const int col = row % 16;
-  unsigned char *block = a.xprep + static_cast<size_t>(m_block) * steps * tt * 128 * 16;
+  // operand layout (prepare_x_kernel's): row-major [row][width] e4m3, so the row's bytes are
+  // whole cache lines of this workgroup's own
+  unsigned char *operand = a.xprep + static_cast<size_t>(row) * a.width;
 #pragma unroll
   for (int i = 0; i < Q; ++i) {
     const int q = threadIdx.x + i * kThreads;
     if (q >= quads) continue;
-    const int k = q * 4;
-    const int step = k / 128, half = (k / 64) % 2, group = (k / 16) % 4;
-    const size_t chunk = ((static_cast<size_t>(step) * tt + tile) * 2 + half) * 64 + group * 16 + col;
-    *reinterpret_cast<uint32_t *>(block + chunk * 16 + (k % 16)) =
+    reinterpret_cast<uint2 *>(a.r1_out + row_offset)[q] = f32x4_to_bf16(r1v[i]);
+    reinterpret_cast<uint2 *>(a.y_out + row_offset)[q] = f32x4_to_bf16(v[i]);
+    reinterpret_cast<uint32_t *>(operand)[q] =
         f32x4_to_e4m3x4(v[i][0] * q_inv, v[i][1] * q_inv, v[i][2] * q_inv, v[i][3] * q_inv);
   }
 }
@@ -623,7 +622,7 @@ LayerEndShape layer_end_shape(const RowArgs &a) {
 
 bool fused_quantization_fits(const RowArgs &a, const LayerEndShape &s) {
   return s.fixed && s.scaled && s.q != 0 && a.rows <= kFusedQuantizeRows && a.y_amax != nullptr &&
-         a.width % 128 == 0 && (a.xprep_token_tiles == 2 || a.xprep_token_tiles == 8);
+         a.width % 128 == 0;
 }
 
 // The layer-end shape of the verify step (see layer_end_kernel); false when it does not apply.

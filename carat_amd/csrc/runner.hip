@@ -1083,7 +1083,6 @@ struct BatchModelRunner::Implementation {
     // Each layer-end row quantises its output only where the row kernel has the fused shape
     // (otherwise the next GEMM prepares its operand itself, with the same bytes).
     auto fuse_quantize = [&](RowArgs &r, int which) {
-      r.xprep_token_tiles = gemm_token_tiles(rows);
       if (!io.fused_quantize || spec.fp8_scaling != 0 || !row_kernel_can_fuse_quantization(r))
         return false;
       r.xprep = xprep.as<unsigned char>();
