@@ -79,6 +79,9 @@ struct GemmArgs {
   int32_t *argmax_table = nullptr;
   int argmax_table_stride = 0;
   int argmax_table_column = 0;
+  // argmax: leave the partial keys for the caller to reduce (no reduction kernel; argmax_out and
+  // the table are not written)
+  bool argmax_deferred = false;
   // e4m3 GEMMs only: activation operand workspace (gemm_xprep_bytes); bf16 GEMMs read x directly
   unsigned char *xprep = nullptr;
   size_t xprep_capacity = 0;

@@ -767,7 +767,7 @@ void launch_gemm(const GemmArgs &a, hipStream_t stream) {
     if (a.partial == nullptr) throw std::runtime_error("GEMM partial output missing");
     break;
   case GemmEpilogue::argmax:
-    if (a.argmax_partials == nullptr || a.k_splits != 1 || a.argmax_out == nullptr)
+    if (a.argmax_partials == nullptr || a.k_splits != 1 || (a.argmax_out == nullptr && !a.argmax_deferred))
       throw std::runtime_error("GEMM argmax needs partial keys, output, 1 split");
     if (static_cast<size_t>(blocks_n) * a.m > a.argmax_partial_capacity)
       throw std::runtime_error("GEMM argmax partial workspace too small");
@@ -814,9 +814,10 @@ prepare_x_kernel<<<grid, 256, 0, stream>>>(a.x, a.ldx, a.m, a.k, a.x_amax, a.ama
   case GemmEpilogue::argmax:
     launch_shape<kFp8, GemmEpilogue::argmax>(a, small_m, group4, grid, stream);
     if (a.timing_stop != nullptr) hip_check(hipEventRecord(a.timing_stop, stream), "record probe");
-    argmax_reduce_kernel<<<a.m, 256, 0, stream>>>(a.argmax_partials, blocks_n, a.argmax_out,
-                                                  a.argmax_table, a.argmax_table_stride,
-                                                  a.argmax_table_column);
+    if (!a.argmax_deferred)
+      argmax_reduce_kernel<<<a.m, 256, 0, stream>>>(a.argmax_partials, blocks_n, a.argmax_out,
+                                                    a.argmax_table, a.argmax_table_stride,
+                                                    a.argmax_table_column);
     break;
   case GemmEpilogue::gelu_gate:
     launch_shape<kFp8, GemmEpilogue::gelu_gate>(a, small_m, group4, grid, stream);

@@ -133,36 +133,113 @@ struct AssistantLayer {
 // [embedding(token) * bf16(sqrt(H)) | previous hidden] (embedding_batch_bf16 +
 // concatenate_rows_bf16, assistant_runner.cu:289-293); with `amax`, also the striped amax of the
 // row (the quantisation of the pre-projection input in AssistantFp8Mode::all).
-__global__ void assistant_input_kernel(const bf16_t *embedding, const int32_t *tokens,
-                                       const bf16_t *previous, bf16_t *out, int rows, int hidden,
-                                       int vocabulary, float scale, float *amax, int stripes) {
-  const int row = blockIdx.y;
-  const bf16_t s = f32_to_bf16(scale);
-  const int token = tokens[row];
-  float maximum = 0.0f;
-  for (int c = blockIdx.x * blockDim.x + threadIdx.x; c < 2 * hidden; c += gridDim.x * blockDim.x) {
-    bf16_t v;
-    if (c < hidden)
-      v = (token >= 0 && token < vocabulary)
-              ? f32_to_bf16(bf16_to_f32(embedding[static_cast<size_t>(token) * hidden + c]) *
-                            bf16_to_f32(s))
-              : static_cast<bf16_t>(0);
-    else
-      v = previous[static_cast<size_t>(row) * hidden + (c - hidden)];
-    out[static_cast<size_t>(row) * 2 * hidden + c] = v;
-    maximum = fmaxf(maximum, fabsf(bf16_to_f32(v)));
-  }
-  if (amax == nullptr) return;  // uniform over the launch
-  maximum = wave_max(maximum);
-  if ((threadIdx.x & (kWave - 1)) == 0) amax_publish(amax, stripes, maximum);
-}
+// The assistant's input row of one draft step (assistant_runner.cu:272-277): the token's
+// embedding row times bf16(sqrt(H)) | the previous hidden row. The token is given, or (the steps
+// after an lm_head pass) reduced here from that pass's per-workgroup argmax keys (the reduction of
+// argmax_reduce_kernel), the row's block 0 writing it to the proposals table. The previous hidden
+// row is gathered from the target's hand-off rows by slot (the first step), or summed here from
+// the post-projection's split-K partials and rounded, as the row kernel would (the later steps).
+// Every thread owns 8 consecutive elements of the 2H-wide row; `amax` (the `all` fp8 mode) gets
+// the row's maximum magnitude.
+struct AssistantInputArgs {
+  const bf16_t *embedding = nullptr;
+  int vocabulary = 0;
+  float embed_scale = 1.0f;
+  const int32_t *tokens = nullptr;             // or:
+  const uint64_t *argmax_partials = nullptr;   // [row][argmax_parts] keys
+  int argmax_parts = 0;
+  int32_t *table = nullptr;                    // optional: table[row * stride + column] = token
+  int table_stride = 0, table_column = 0;
+  const bf16_t *gather_src = nullptr;          // [slot][hidden], rows gather_rows[row]; or:
+  const int32_t *gather_rows = nullptr;
+  const float *partials = nullptr;             // [splits][rows][hidden]
+  int splits = 1;
+  const float *x_amax = nullptr;               // partials' fp8 output scale operands (or null)
+  const float *w_scale = nullptr;
+  bf16_t *out = nullptr;                       // [rows][2 hidden]
+  int rows = 0, hidden = 0;
+  float *amax = nullptr;
+  int stripes = 1;
+};
 
-__global__ void gather_rows_kernel(const bf16_t *in, const int32_t *rows_index, bf16_t *out,
-                                   int width) {
+__global__ __launch_bounds__(256) void assistant_input_kernel(const AssistantInputArgs a) {
   const int row = blockIdx.y;
-  const size_t src = static_cast<size_t>(rows_index[row]) * width;
-  for (int c = blockIdx.x * blockDim.x + threadIdx.x; c < width; c += gridDim.x * blockDim.x)
-    out[static_cast<size_t>(row) * width + c] = in[src + c];
+  const int c0 = (blockIdx.x * 256 + threadIdx.x) * 8;
+  const bool live = c0 < 2 * a.hidden;
+  const bool previous = live && c0 >= a.hidden;
+  // the previous-hidden half first: its loads do not wait for the token
+  float pv[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  u32x4_t gathered = {0u, 0u, 0u, 0u};
+  float amax_part = 0.0f, w_scale = 1.0f;
+  if (a.partials != nullptr) {
+    if (a.x_amax != nullptr) amax_part = amax_lane(a.x_amax, a.stripes);
+    if (a.w_scale != nullptr) w_scale = *a.w_scale;
+  }
+  if (previous) {
+    const int c = c0 - a.hidden;
+    if (a.partials != nullptr) {
+      for (int k = 0; k < a.splits; ++k) {
+        const float *src = a.partials + (static_cast<size_t>(k) * a.rows + row) * a.hidden + c;
+        const f32x4_t lo = *reinterpret_cast<const f32x4_t *>(src);
+        const f32x4_t hi = *reinterpret_cast<const f32x4_t *>(src + 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          pv[e] += lo[e];
+          pv[4 + e] += hi[e];
+        }
+      }
+    } else {
+      gathered = *reinterpret_cast<const u32x4_t *>(
+          a.gather_src + static_cast<size_t>(a.gather_rows[row]) * a.hidden + c);
+    }
+  }
+  int token;
+  if (a.argmax_partials != nullptr) {
+    uint64_t best = kArgmaxInitialKey;
+    for (int i = threadIdx.x; i < a.argmax_parts; i += 256) {
+      const uint64_t k = a.argmax_partials[static_cast<size_t>(row) * a.argmax_parts + i];
+      best = k > best ? k : best;
+    }
+    best = wave_max_u64(best);
+    __shared__ uint64_t wave_best[4];
+    if ((threadIdx.x & 63) == 0) wave_best[threadIdx.x >> 6] = best;
+    __syncthreads();
+    best = wave_best[0];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) best = wave_best[w] > best ? wave_best[w] : best;
+    token = static_cast<int>(argmax_key_index(best));
+  } else {
+    token = a.tokens[row];
+  }
+  if (a.table != nullptr && blockIdx.x == 0 && threadIdx.x == 0)
+    a.table[row * a.table_stride + a.table_column] = token;
+  float scale = w_scale;
+  if (a.partials != nullptr && a.x_amax != nullptr) scale *= fp8_scale_from_amax(wave_max(amax_part));
+  if (!live) return;
+  u32x4_t value;
+  if (!previous) {
+    value = u32x4_t{0u, 0u, 0u, 0u};
+    if (token >= 0 && token < a.vocabulary) {
+      const float s = round_bf16(a.embed_scale);
+      const u32x4_t e = *reinterpret_cast<const u32x4_t *>(a.embedding + static_cast<size_t>(token) * a.hidden + c0);
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        value[q] = f32x2_to_bf16x2(__uint_as_float(e[q] << 16) * s, __uint_as_float(e[q] & 0xffff0000u) * s);
+    }
+  } else if (a.partials != nullptr) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) value[q] = f32x2_to_bf16x2(pv[2 * q] * scale, pv[2 * q + 1] * scale);
+  } else {
+    value = gathered;
+  }
+  *reinterpret_cast<u32x4_t *>(a.out + static_cast<size_t>(row) * 2 * a.hidden + c0) = value;
+  if (a.amax == nullptr) return;
+  float maximum = 0.0f;
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+    maximum = fmaxf(maximum, fmaxf(fabsf(__uint_as_float(value[q] << 16)), fabsf(__uint_as_float(value[q] & 0xffff0000u))));
+  maximum = wave_max(maximum);
+  if ((threadIdx.x & (kWave - 1)) == 0) amax_publish(a.amax, a.stripes, maximum);
 }
 
 __global__ void copy_tokens_kernel(const int32_t *src, int32_t *dst, int32_t *table, int rows,
@@ -226,6 +303,7 @@ struct BatchModelRunner::Implementation {
           *d_caps = nullptr, *d_accepted = nullptr, *d_next = nullptr, *d_predictions = nullptr,
           *d_fault = nullptr;
   int32_t *host_io = nullptr;  // pinned mirror of device_io
+  int32_t *a_host_io = nullptr;  // pinned mirror of a_io (the draft's inputs and proposals)
   // verify steps quantise the layer-end rows' outputs in the row kernels (RowArgs::xprep)
   // 0 (default): separate prepare kernels, measured faster in the step than the fused
   // quantisation (1); 2: fused with a zero wait bound (error-path test)
@@ -339,6 +417,8 @@ struct BatchModelRunner::Implementation {
     verify_graphs.clear();
     if (host_io != nullptr) (void)hipHostFree(host_io);
     host_io = nullptr;
+    if (a_host_io != nullptr) (void)hipHostFree(a_host_io);
+    a_host_io = nullptr;
     if (start_event != nullptr) (void)hipEventDestroy(start_event);
     if (stop_event != nullptr) (void)hipEventDestroy(stop_event);
     start_event = stop_event = nullptr;
@@ -741,6 +821,8 @@ struct BatchModelRunner::Implementation {
     a_final_hidden.allocate(sizeof(bf16_t) * B * AH);
     a_previous_hidden.allocate(sizeof(bf16_t) * B * H);
     a_io.allocate(sizeof(int32_t) * B * (5 + kMaximumDepth));
+    hip_check(hipHostMalloc(reinterpret_cast<void **>(&a_host_io), sizeof(int32_t) * B * (5 + kMaximumDepth)),
+              "allocate pinned assistant staging");
     a_tokens = a_io.as<int32_t>();
     a_outputs = a_tokens + B;
     a_forced = a_outputs + B;
@@ -1905,15 +1987,17 @@ struct BatchModelRunner::Implementation {
         throw std::runtime_error("invalid assistant row metadata");
     }
     const size_t B = static_cast<size_t>(batch_size);
-    std::vector<int32_t> staging(B * 5, 0);
+    // inputs: tokens[B] outputs[B] forced[B] context[B] slots[B] (the prefix of the I/O block), by
+    // DMA from its pinned mirror
+    int32_t *staging = a_host_io;
+    std::fill(staging, staging + B * 5, 0);
     for (int row = 0; row < active; ++row) {
       staging[static_cast<size_t>(row)] = last_tokens[static_cast<size_t>(row)];
       if (!forced.empty()) staging[2 * B + static_cast<size_t>(row)] = forced[static_cast<size_t>(row)];
       staging[3 * B + static_cast<size_t>(row)] = context_positions[static_cast<size_t>(row)];
       staging[4 * B + static_cast<size_t>(row)] = slots[static_cast<size_t>(row)];
     }
-    hip_check(hipMemcpyAsync(a_tokens, staging.data(), sizeof(int32_t) * staging.size(),
-                             hipMemcpyHostToDevice, stream),
+    hip_check(hipMemcpyAsync(a_tokens, staging, sizeof(int32_t) * B * 5, hipMemcpyHostToDevice, stream),
               "copy assistant inputs");
     hip_check(hipEventRecord(start_event, stream), "record draft start");
     const AssistantSpec &as = spec.assistant;
@@ -1924,24 +2008,51 @@ struct BatchModelRunner::Implementation {
       launch_step_init(a_amax.as<float>(),
                        static_cast<int>(depth * assistant_amax_slots_per_step() * kAmaxStripes),
                        stream);
-    {
-      // previous_hidden = target_hidden_by_slot[slots]
-      const dim3 grid(std::max(1, std::min(32, (H + 255) / 256)), active);
-      gather_rows_kernel<<<grid, 256, 0, stream>>>(target_hidden.as<bf16_t>(), a_slots,
-                                                   a_previous_hidden.as<bf16_t>(), H);
-      hip_check(hipGetLastError(), "launch gather rows");
-    }
+    if (H % 8 != 0) throw std::runtime_error("assistant input rows need a hidden size divisible by 8");
+    // Argmax keys per row of the assistant lm_head (its workgroup feature blocks).
+    const int argmax_parts = gemm_blocks_n(assistant_fp8 != 0 ? a_embedding8.layout : a_embedding.layout);
+    int post_splits = 0;  // split-K partials of the previous step's post-projection (0: none)
+    bool previous_lm_head = false;  // the previous step ran the lm_head (else its token was forced)
     for (int d = 0; d < depth; ++d) {
-      const int32_t *input_tokens = d == 0 ? a_tokens : a_outputs;
       {
-        const dim3 grid(std::max(1, std::min(64, (2 * H + 255) / 256)), active);
-        assistant_input_kernel<<<grid, 256, 0, stream>>>(
-            embedding_bf16.as<bf16_t>(), input_tokens, a_previous_hidden.as<bf16_t>(),
-            a_input.as<bf16_t>(), active, H, spec.vocabulary, std::sqrt(static_cast<float>(H)),
-            all8 ? assistant_amax(d, 0) : nullptr, stripes);
+        // step 0: the given tokens and the target's hand-off rows (gather_rows_bf16 by slot);
+        // later steps: the previous step's token (argmax keys, or the forced token) and the sum
+        // of its post-projection partials
+        AssistantInputArgs in;
+        in.embedding = embedding_bf16.as<bf16_t>();
+        in.vocabulary = spec.vocabulary;
+        in.embed_scale = std::sqrt(static_cast<float>(H));
+        if (d == 0) {
+          in.tokens = a_tokens;
+          in.gather_src = target_hidden.as<bf16_t>();
+          in.gather_rows = a_slots;
+        } else {
+          if (previous_lm_head) {
+            in.argmax_partials = argmax_partials.as<uint64_t>();
+            in.argmax_parts = argmax_parts;
+          } else {
+            in.tokens = a_forced;  // assistant_runner.cu:306-312
+          }
+          in.table = a_proposals;
+          in.table_stride = depth;
+          in.table_column = d - 1;
+          in.partials = partials.as<float>();
+          in.splits = post_splits;
+          if (all8) {
+            in.x_amax = assistant_final_amax(d - 1);
+            in.w_scale = a_scales8.as<float>() + 2;
+          }
+        }
+        in.out = a_input.as<bf16_t>();
+        in.rows = active;
+        in.hidden = H;
+        in.amax = all8 ? assistant_amax(d, 0) : nullptr;
+        in.stripes = stripes;
+        const dim3 grid(static_cast<unsigned>((2 * H / 8 + 255) / 256), static_cast<unsigned>(active));
+        assistant_input_kernel<<<grid, 256, 0, stream>>>(in);
         hip_check(hipGetLastError(), "launch assistant input");
       }
-      int splits = run_assistant_partial(a_input.as<bf16_t>(), active, 2 * H, a_pre_projection,
+      const int splits = run_assistant_partial(a_input.as<bf16_t>(), active, 2 * H, a_pre_projection,
                                          a_pre_projection8,
                                          all8 ? a_scales8.as<float>() + 1 : nullptr,
                                          all8 ? assistant_amax(d, 0) : nullptr);
@@ -1968,11 +2079,16 @@ struct BatchModelRunner::Implementation {
         run_assistant_layer(li, input, output, active, d, li + 1 == assistant_layers.size());
         std::swap(input, output);
       }
-      if (d == 0 && !forced.empty()) {
-        // assistant_runner.cu:306-312: the forced token replaces the dead first lm_head pass.
-        copy_tokens_kernel<<<(active + 255) / 256, 256, 0, stream>>>(a_forced, a_outputs,
-                                                                     a_proposals, active, depth, d);
-        hip_check(hipGetLastError(), "launch forced tokens");
+      const bool last = d + 1 == depth;
+      previous_lm_head = !(d == 0 && !forced.empty());
+      if (!previous_lm_head) {
+        // assistant_runner.cu:306-312: the forced token replaces the dead first lm_head pass (the
+        // next step's input kernel writes it to the table; a one-step draft does it here)
+        if (last) {
+          copy_tokens_kernel<<<(active + 255) / 256, 256, 0, stream>>>(a_forced, a_outputs,
+                                                                       a_proposals, active, depth, d);
+          hip_check(hipGetLastError(), "launch forced tokens");
+        }
       } else {
         GemmArgs g;
         g.x = a_final_hidden.as<bf16_t>();
@@ -1995,6 +2111,8 @@ struct BatchModelRunner::Implementation {
         g.epilogue = GemmEpilogue::argmax;
         g.argmax_partials = argmax_partials.as<uint64_t>();
         g.argmax_partial_capacity = argmax_partials.bytes() / sizeof(uint64_t);
+        // the next step's input kernel reduces the keys; the last step's go to the table here
+        g.argmax_deferred = !last;
         g.argmax_out = a_outputs;
         g.argmax_table = a_proposals;
         g.argmax_table_stride = depth;
@@ -2004,27 +2122,31 @@ struct BatchModelRunner::Implementation {
         else
           launch_bf16_gemm(g, stream);
       }
-      splits = run_assistant_partial(a_final_hidden.as<bf16_t>(), active, as.hidden,
-                                     a_post_projection, a_post_projection8,
-                                     all8 ? a_scales8.as<float>() + 2 : nullptr,
-                                     assistant_final_amax(d));
-      RowArgs rq;
-      rq.amax_stripes = stripes;
-      if (all8) {
-        rq.x_amax = assistant_final_amax(d);
-        rq.w_scale = a_scales8.as<float>() + 2;
+      post_splits = run_assistant_partial(a_final_hidden.as<bf16_t>(), active, as.hidden,
+                                          a_post_projection, a_post_projection8,
+                                          all8 ? a_scales8.as<float>() + 2 : nullptr,
+                                          assistant_final_amax(d));
+      if (last) {
+        // the last step's hand-off row (assistant.previous_hidden); earlier ones are summed by the
+        // next step's input kernel
+        RowArgs rq;
+        rq.amax_stripes = stripes;
+        if (all8) {
+          rq.x_amax = assistant_final_amax(d);
+          rq.w_scale = a_scales8.as<float>() + 2;
+        }
+        rq.source = RowSource::partials;
+        rq.rows = active;
+        rq.width = H;
+        rq.partials = partials.as<float>();
+        rq.splits = post_splits;
+        rq.v_out = a_previous_hidden.as<bf16_t>();
+        launch_row_kernel(rq, stream);
       }
-      rq.source = RowSource::partials;
-      rq.rows = active;
-      rq.width = H;
-      rq.partials = partials.as<float>();
-      rq.splits = splits;
-      rq.v_out = a_previous_hidden.as<bf16_t>();
-      launch_row_kernel(rq, stream);
     }
     hip_check(hipEventRecord(stop_event, stream), "record draft stop");
-    std::vector<int32_t> table(static_cast<size_t>(active) * depth);
-    hip_check(hipMemcpyAsync(table.data(), a_proposals, sizeof(int32_t) * table.size(),
+    int32_t *table = a_host_io + 5 * B;  // the pinned mirror of a_proposals
+    hip_check(hipMemcpyAsync(table, a_proposals, sizeof(int32_t) * static_cast<size_t>(active) * depth,
                              hipMemcpyDeviceToHost, stream),
               "copy assistant proposals");
     hip_check(hipStreamSynchronize(stream), "synchronize assistant draft");
