@@ -20,10 +20,11 @@ enum class GemmEpilogue : int {
 };
 
 // Weight storage. Weights stream HBM -> VGPRs exactly once per launch, so they are stored in the
-// order the kernel reads them: feature rows are grouped into workgroup blocks of 4 * F tiles of 16
-// rows (F = tiles per wave), and the block's 4 * F tiles of one 128-byte K step form one
-// contiguous 4 * F * 2 KiB run: packed[block][step][tile][half][lane][16 B], lane = g * 16 + c
-// holding row (tile row c) bytes [step * 128 + half * 64 + g * 16, +16). A gate/up weight
+// order the kernel reads them: feature rows are grouped into workgroup blocks of W * F tiles of 16
+// rows (F = tiles per wave, W waves), and the block's W * F tiles of one 128-byte K step form one
+// contiguous W * F * 2 KiB run: packed[step][block][tile][half][lane][16 B] (step-major, so that
+// the runs of one K step of all blocks are contiguous; packed[block][step][...] with step_major
+// false), lane = g * 16 + c holding row (tile row c) bytes [step * 128 + half * 64 + g * 16, +16). A gate/up weight
 // ([gate rows | up rows], cuda/ops.cu:264-270) puts F/2 gate tiles and the matching F/2 up tiles
 // in each wave. The logical matrix stays [N][row_bytes] (pack_weight / unpack_weight convert).
 struct WeightLayout {
@@ -32,6 +33,9 @@ struct WeightLayout {
   int tiles_per_wave = 1;  // F: 1, 2 or 4 (even for gate/up)
   int waves = 4;           // W: waves per workgroup, 3 or 4 (1 or 2 for few-row weights)
   bool gate_up = false;
+  // Step-major order: packed[step][block][...] instead of packed[block][step][...], so that the
+  // workgroups of one K step read one contiguous run of the weight.
+  bool step_major = false;
 };
 
 // Storage layout for an [n][row_bytes] weight: the widest F that still leaves >= 64 workgroups.

@@ -44,7 +44,7 @@ __device__ __forceinline__ float gelu_tanh(float v) {
 // weight packing: one thread per 16-byte chunk of the packed layout
 // ---------------------------------------------------------------------------------------------
 struct PackGeometry {
-  int n, row_bytes, f, waves, gate_up, steps, group_tiles;
+  int n, row_bytes, f, waves, gate_up, steps, group_tiles, blocks, step_major;
 };
 
 // Logical (row, byte offset) of packed 16-byte chunk `chunk`.
@@ -55,8 +55,8 @@ __device__ __forceinline__ void packed_chunk_source(const PackGeometry &g, size_
   size_t rest = chunk >> 7;
   const int tile = static_cast<int>(rest % g.group_tiles);
   rest /= g.group_tiles;
-  const int step = static_cast<int>(rest % g.steps);
-  const int block = static_cast<int>(rest / g.steps);
+  const int step = static_cast<int>(g.step_major ? rest / g.blocks : rest % g.steps);
+  const int block = static_cast<int>(g.step_major ? rest % g.blocks : rest / g.steps);
   const int col = lane & 15;
   if (g.gate_up) {
     const int h = g.f / 2;
@@ -98,7 +98,8 @@ void launch_pack(const void *src, void *dst, const WeightLayout &l, bool pack, h
   check_layout(l);
   if (src == nullptr || dst == nullptr) throw std::runtime_error("null weight pointer");
   const PackGeometry g{l.n, l.row_bytes, l.tiles_per_wave, l.waves, l.gate_up ? 1 : 0,
-                       l.row_bytes / kStepBytes, l.waves * l.tiles_per_wave};
+                       l.row_bytes / kStepBytes, l.waves * l.tiles_per_wave,
+                       l.n / (16 * l.waves * l.tiles_per_wave), l.step_major ? 1 : 0};
   const size_t chunks = static_cast<size_t>(l.n) * l.row_bytes / 16;
   const unsigned blocks = static_cast<unsigned>(std::min<size_t>((chunks + 255) / 256, 65536));
   if (pack)
@@ -297,6 +298,10 @@ void gemm_kernel(const GemmArgs a) {
   // gelu_gate: tiles [0, F/2) are gate rows, [F/2, F) the matching up rows of the packed
   // [gate | up] weight (cuda/ops.cu:264-270 packing).
   constexpr int kGroupBytes = W * FL * kTileBytes;  // one K step of one layout block
+  // step-major weights: one K step of all layout blocks is contiguous
+  const int layout_blocks = a.n / (16 * W * FL);
+  const size_t step_stride = a.w_layout.step_major ? static_cast<size_t>(layout_blocks) * kGroupBytes
+                                                   : static_cast<size_t>(kGroupBytes);
   const unsigned char *wrow[F];
   int feature0[F];
 #pragma unroll
@@ -309,8 +314,10 @@ void gemm_kernel(const GemmArgs a) {
     } else {
       feature0[f] = block * (16 * W * FL) + tile * 16;
     }
-    wrow[f] = static_cast<const unsigned char *>(a.w) +
-              (static_cast<size_t>(block) * total_steps + step0) * kGroupBytes + tile * kTileBytes + lane * 16;
+    const size_t run = a.w_layout.step_major
+                           ? static_cast<size_t>(step0) * layout_blocks + block
+                           : static_cast<size_t>(block) * total_steps + step0;
+    wrow[f] = static_cast<const unsigned char *>(a.w) + run * kGroupBytes + tile * kTileBytes + lane * 16;
   }
   // Weight scale row of tile f (gelu_gate: the up tiles are rows n/2 + feature0).
   auto scale_row = [&](int f) {
@@ -366,7 +373,7 @@ void gemm_kernel(const GemmArgs a) {
           16, 0, 0);
 #pragma unroll
     for (int f = 0; f < F; ++f) {
-      const unsigned char *src = wrow[f] + static_cast<size_t>(s) * kGroupBytes;
+      const unsigned char *src = wrow[f] + static_cast<size_t>(s) * step_stride;
       wreg[slot][f][0] = *reinterpret_cast<const u32x4 *>(src);
       wreg[slot][f][1] = *reinterpret_cast<const u32x4 *>(src + 1024);
     }
@@ -864,6 +871,11 @@ WeightLayout gemm_weight_layout(int n, int row_bytes, bool gate_up, bool few_row
   // GEMMs of a few rows per call (the assistant's draft step, 24 rows) are latency-bound: when
   // the grid stays small, narrower workgroups (fewer waves, the same F) give more of them -- the
   // widest that reaches 240 workgroups with its split-K factor, else one wave.
+  // Step-major storage: at any moment the workgroups stream one contiguous window of the weight
+  // (the K step they are at) instead of 224-1024 runs a block's whole K range apart (measured on
+  // MI355X, config-5 verify over four pairs of runners: 13.53 -> 13.18 ms median, every pair
+  // faster; the GEMMs timed back to back alone do not change).
+  l.step_major = true;
   if (few_rows) {
     const int steps = row_bytes / 128;
     auto workgroups = [&](int w) {
