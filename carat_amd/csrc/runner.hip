@@ -130,17 +130,16 @@ struct AssistantLayer {
   DeviceBuffer scales8;
 };
 
-// [embedding(token) * bf16(sqrt(H)) | previous hidden] (embedding_batch_bf16 +
-// concatenate_rows_bf16, assistant_runner.cu:289-293); with `amax`, also the striped amax of the
-// row (the quantisation of the pre-projection input in AssistantFp8Mode::all).
-// The assistant's input row of one draft step (assistant_runner.cu:272-277): the token's
-// embedding row times bf16(sqrt(H)) | the previous hidden row. The token is given, or (the steps
-// after an lm_head pass) reduced here from that pass's per-workgroup argmax keys (the reduction of
+// The assistant's input row of one draft step: the token's embedding row times bf16(sqrt(H)) |
+// the previous hidden row (embedding_batch_bf16 + concatenate_rows_bf16,
+// assistant_runner.cu:279-283). The token is given, or (the steps after an lm_head pass) reduced
+// here from that pass's per-workgroup argmax keys (argmax_bf16_rows, :316; the reduction of
 // argmax_reduce_kernel), the row's block 0 writing it to the proposals table. The previous hidden
-// row is gathered from the target's hand-off rows by slot (the first step), or summed here from
-// the post-projection's split-K partials and rounded, as the row kernel would (the later steps).
-// Every thread owns 8 consecutive elements of the 2H-wide row; `amax` (the `all` fp8 mode) gets
-// the row's maximum magnitude.
+// row is gathered from the target's hand-off rows by slot (gather_rows_bf16, :271; the first
+// step), or summed here from the post-projection's split-K partials and rounded as the row kernel
+// would (:320; the later steps). Every thread owns 8 consecutive elements of the 2H-wide row;
+// `amax` (the `all` fp8 mode: the pre-projection input's per-tensor quantisation) gets the row's
+// maximum magnitude.
 struct AssistantInputArgs {
   const bf16_t *embedding = nullptr;
   int vocabulary = 0;
